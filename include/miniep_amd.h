@@ -1,0 +1,187 @@
+/*
+ * miniep_amd.h -- C ABI of the MI355X (gfx950) MoE-block hot path.
+ *
+ * The reference (mini-EP) runs the GraniteMoE MoE block as PyTorch CPU ops
+ * behind a per-layer "MoE backend" callable
+ *     backend(x_flat (N,H), topk_idx (N,k) int64, topk_gate (N,k), valid_mask (N,) bool|None) -> (N,H)
+ * (miniep/modeling.py:131-145, used at :196; the expert-parallel drop-in is
+ * miniep/ep.py:186-249) with the router inline in Block.forward
+ * (miniep/modeling.py:192-195).  This library replaces the arithmetic of that
+ * seam with four hand-written HIP kernel groups:
+ *
+ *   mep_router_topk     router GEMV + top-k + softmax      modeling.py:192-195
+ *   mep_topk_softmax    top-k + softmax from fp32 logits   modeling.py:194-195
+ *   mep_dispatch        flatten + histogram + stable rank  modeling.py:94-96,107-117
+ *                       + replica round-robin + rank share ep.py:76-96,203-231
+ *   mep_grouped_swiglu  run_experts (gather, GEMM-1,       modeling.py:83-104
+ *                       SiLU*up, GEMM-2, scatter); also as
+ *                       mep_swiglu_gate_up + mep_swiglu_down
+ *   mep_combine         gate * y, slot-order sum           modeling.py:120-128,144
+ *
+ * Conventions
+ *  - Every pointer argument is DEVICE memory unless marked "host".
+ *  - The library never allocates: buffers, including workspaces, come from
+ *    the caller (size queries below).
+ *  - Work is enqueued on `stream` (a hipStream_t; NULL = default stream).
+ *    No call synchronises the stream except mep_dispatch_check().
+ *  - Every call returns 0 on success or a negative MEP_ERR_* code; the message
+ *    of the last failure on the calling thread is in mep_last_error().
+ *  - Layouts are row-major and dense.  Expert weights follow the checkpoint
+ *    layout (miniep/weights.py:17-26): w_in (E_local, 2I, H) = [gate rows | up
+ *    rows], w_out (E_local, H, I), local experts in sorted global-id order
+ *    (miniep/weights.py:54-58).
+ *  - Flat entry id of token t, slot s is f = t*k + s (modeling.py:107-117).
+ */
+#ifndef MINIEP_AMD_H
+#define MINIEP_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* element types of activations / weights / gates / outputs */
+#define MEP_DTYPE_F32 0
+#define MEP_DTYPE_BF16 1
+
+/* return codes */
+#define MEP_OK 0
+#define MEP_ERR_INVALID_ARG (-1)      /* null pointer, negative size, bad dtype   */
+#define MEP_ERR_UNSUPPORTED (-2)      /* shape outside what the kernels support  */
+#define MEP_ERR_WORKSPACE (-3)        /* workspace smaller than the size query    */
+#define MEP_ERR_EXPERT_RANGE (-4)     /* topk_idx outside [0, n_experts)           */
+#define MEP_ERR_NOT_RESIDENT (-5)     /* entry routed here for a non-resident expert (ep.py:230) */
+#define MEP_ERR_HIP (-6)              /* HIP runtime error (launch, sync)          */
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* mep_last_error(void);
+
+/* ABI version of this header (bumped on incompatible changes). */
+int mep_abi_version(void);
+
+/* ------------------------------------------------------------------------
+ * Router: logits = x @ w_router^T, top-k (descending; equal logits: lower
+ * expert id first), gate = softmax over the k selected logits in fp32,
+ * stored in `dtype`.  Replaces modeling.py:193-195.  The logits are
+ * accumulated in fp32 for both dtypes (the reference accumulates in x.dtype);
+ * they are written to `logits` (N, E) fp32 when it is non-NULL.
+ *   x         (N, H) dtype          w_router (E, H) dtype
+ *   topk_idx  (N, k) int64          topk_gate (N, k) dtype
+ * Supported: E in {16, 32, 64}, 1 <= k <= E, H % 256 == 0.
+ * ---------------------------------------------------------------------- */
+int mep_router_topk(const void* x, const void* w_router, int64_t n_tokens,
+                    int32_t hidden, int32_t n_experts, int32_t top_k, int32_t dtype,
+                    int64_t* topk_idx, void* topk_gate, float* logits, void* stream);
+
+/* Top-k + softmax of precomputed fp32 logits (N, E); the selection rule of
+ * mep_router_topk.  Replaces modeling.py:194-195.  E <= 256, 1 <= k <= min(E, 32). */
+int mep_topk_softmax(const float* logits, int64_t n_tokens, int32_t n_experts,
+                     int32_t top_k, int32_t gate_dtype, int64_t* topk_idx,
+                     void* topk_gate, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Dispatch: this GPU's share of the routed entries, stably grouped by local
+ * expert.  Replaces flatten_topk (modeling.py:107-117), the stable argsort /
+ * unique_consecutive of run_experts (modeling.py:94-96), Placement.dest_ranks
+ * (ep.py:76-96) and the receive side of EPMoEBackend (ep.py:216-231).
+ *
+ * The N tokens are the concatenation of S source segments (host array
+ * seg_tokens[0..S], seg_tokens[0] = 0, seg_tokens[S] = N): segment s is what
+ * source rank s sends, with its own round-robin counters rr[s, :] (each
+ * source owns a Placement, ep.py:27-33).  S = 1 is one rank's own dispatch;
+ * world = 1 with table = 0, g2l = identity is LocalMoEBackend.
+ *
+ *   topk_idx    (N, k) int64            valid_mask (N,) uint8 or NULL (= all valid)
+ *   table       (E, rmax) int32  table[e, j] = rank of e's j-th replica (ep.py:35-45)
+ *   n_rep       (E,) int32       >= 1
+ *   has_replicas  0 iff every n_rep[e] == 1; then dest = table[e, 0] and rr
+ *                 is neither read nor written (ep.py:84-85)
+ *   rr          (S, E) int64 in/out, may be NULL iff has_replicas == 0;
+ *               rr[s, e] += #entries of expert e in segment s (ep.py:95)
+ *   my_rank     entries with dest == my_rank are kept
+ *   g2l         (E,) int32 global -> local expert id, -1 if not resident
+ *   n_local     number of local experts (rows of w_in / w_out)
+ * Outputs:
+ *   counts      (n_local,) int32  rows per local expert
+ *   offsets     (n_local + 1,) int32 exclusive prefix of counts
+ *   perm        (N*k,) int32  perm[row] = flat entry id, rows [0, offsets[n_local])
+ *   row_of_entry(N*k,) int32  row of each entry here, -1 if invalid / elsewhere
+ *   dest        (N*k,) int32 or NULL: destination rank, -1 for invalid tokens
+ *   route_counts(E,) int64 or NULL: += per-expert valid-entry counts (ep.py:216-217)
+ * Invalid expert ids are dropped and recorded; kept entries of non-resident
+ * experts are dropped and recorded (ep.py:230 asserts); mep_dispatch_check()
+ * reports them.  Supported: 1 <= k <= 32, E <= 256, S <= 16, N*k < 2^31.
+ * ---------------------------------------------------------------------- */
+size_t mep_dispatch_workspace_size(int64_t n_tokens, int32_t top_k, int32_t n_experts,
+                                   int32_t n_segments, const int64_t* seg_tokens /* host */);
+
+int mep_dispatch(const int64_t* topk_idx, const uint8_t* valid_mask, int64_t n_tokens,
+                 int32_t top_k, int32_t n_experts,
+                 const int32_t* table, const int32_t* n_rep, int32_t rmax,
+                 int32_t has_replicas, int64_t* rr,
+                 const int64_t* seg_tokens /* host */, int32_t n_segments,
+                 int32_t my_rank, const int32_t* g2l, int32_t n_local,
+                 int32_t* counts, int32_t* offsets, int32_t* perm,
+                 int32_t* row_of_entry, int32_t* dest, int64_t* route_counts,
+                 void* workspace, size_t workspace_bytes, void* stream);
+
+/* Synchronises `stream` and returns MEP_ERR_EXPERT_RANGE / MEP_ERR_NOT_RESIDENT
+ * if the last mep_dispatch on `workspace` dropped entries, else MEP_OK. */
+int mep_dispatch_check(const void* workspace, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Grouped SwiGLU experts over the dispatched rows (run_experts,
+ * modeling.py:83-104), fused with the row gather (modeling.py:143) and the
+ * scatter back to entry order:
+ *   for row r of local expert e (offsets[e] <= r < offsets[e+1]):
+ *     f = perm[r];  a = x[f / k]                         (gather)
+ *     h = W_in[e] a;  act = silu(h[:I]) * h[I:]          (GEMM-1 + SwiGLU)
+ *     y_entries[f] = W_out[e] act                        (GEMM-2 + scatter)
+ * fp32 accumulation; act and y are stored in `dtype`.  Rows of entries that
+ * are not dispatched here are left untouched.
+ *   x (N, H)   w_in (n_local, 2I, H)   w_out (n_local, H, I)   y_entries (N*k, H)
+ * max_rows >= offsets[n_local] (e.g. N*k) bounds the launch.
+ * Supported: H % 256 == 0, I % 128 == 0.
+ * ---------------------------------------------------------------------- */
+size_t mep_experts_workspace_size(int64_t max_rows, int32_t inter, int32_t dtype);
+
+int mep_grouped_swiglu(const void* x, int64_t n_tokens, int32_t top_k,
+                       const int32_t* perm, const int32_t* offsets, int32_t n_local,
+                       int64_t max_rows, const void* w_in, const void* w_out,
+                       int32_t hidden, int32_t inter, int32_t dtype, void* y_entries,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
+/* The two launches of mep_grouped_swiglu as separate calls, for callers that
+ * schedule or time them individually (same kernels, same results):
+ *   mep_swiglu_gate_up  GEMM-1 + SwiGLU: act[r] = silu(W_g x) * (W_u x), x = x[perm[r]/k]
+ *                       act (max_rows, inter) in `dtype`, act_bytes >= max_rows*inter*elem
+ *   mep_swiglu_down     GEMM-2 + scatter: y_entries[perm[r]] = W_out act[r]
+ * Replace modeling.py:101-102 and :103 respectively. */
+int mep_swiglu_gate_up(const void* x, int64_t n_tokens, int32_t top_k, const int32_t* perm,
+                       const int32_t* offsets, int32_t n_local, int64_t max_rows,
+                       const void* w_in, int32_t hidden, int32_t inter, int32_t dtype,
+                       void* act, size_t act_bytes, void* stream);
+
+int mep_swiglu_down(const void* act, int64_t n_tokens, int32_t top_k, const int32_t* perm,
+                    const int32_t* offsets, int32_t n_local, int64_t max_rows,
+                    const void* w_out, int32_t hidden, int32_t inter, int32_t dtype,
+                    void* y_entries, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Combine: out[t] = sum_{s=0..k-1, row_of_entry[t*k+s] >= 0} gate[t,s] * y_entries[t*k+s]
+ * summed in slot order in fp32, stored in `dtype`; invalid tokens give 0.
+ * Replaces the gate multiply (modeling.py:144 / ep.py:241) and
+ * scatter_combine (modeling.py:120-128).
+ *   y_entries (N*k, H)  topk_gate (N, k)  row_of_entry (N*k,) int32  out (N, H)
+ * Supported: H % 8 == 0 (bf16) / H % 4 == 0 (fp32).
+ * ---------------------------------------------------------------------- */
+int mep_combine(const void* y_entries, const void* topk_gate, const int32_t* row_of_entry,
+                const uint8_t* valid_mask, int64_t n_tokens, int32_t top_k,
+                int32_t hidden, int32_t dtype, void* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MINIEP_AMD_H */

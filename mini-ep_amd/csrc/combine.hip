@@ -1,0 +1,130 @@
+// Combine / unpermute for the MoE block.
+//
+// Replaces the gate multiply and scatter_combine of the reference
+// (modeling.py:144, :120-128; ep.py:239-242):
+//     gated = outs * topk_gate[keep].unsqueeze(1)
+//     buf = zeros(n, k, H); buf[token_ids, slot_ids] = gated; out = buf.sum(dim=1)
+// GEMM-2 already wrote every expert output row to its (token, slot) cell of
+// y_entries (the reference's `buf` layout), so the combine is a streaming
+// reduction: each thread owns 16 bytes of one token's output row, loads the
+// k cells of that token (k x 16 B, all in flight), and sums gate * y in slot
+// order in fp32 -- the same fixed order on every run, no atomics.
+#include "common.h"
+
+namespace mep {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kMaxK = 32;
+constexpr int kStage = 1024;   // staged (token, slot) cells per block
+
+template <int DT>
+__global__ __launch_bounds__(kThreads) void combine_kernel(const typename Elem<DT>::T* __restrict__ y,
+                                                           const typename Elem<DT>::T* __restrict__ gate,
+                                                           const int32_t* __restrict__ row_of_entry,
+                                                           const uint8_t* __restrict__ valid,
+                                                           int64_t n_tokens, int k, int hidden,
+                                                           typename Elem<DT>::T* __restrict__ out) {
+  typedef typename Elem<DT>::T T;
+  constexpr int EPC = 16 / Elem<DT>::kBytes;
+  const int tpt = hidden / EPC;                         // threads per token
+  const int tokens_per_block = kThreads / tpt;
+  __shared__ float s_gate[kStage];                      // [tokens_per_block * k]
+  __shared__ uint8_t s_here[kStage];
+  const int tid = threadIdx.x;
+  const int local_tok = tid / tpt;
+  const int c = tid - local_tok * tpt;
+  const int64_t tok0 = static_cast<int64_t>(blockIdx.x) * tokens_per_block;
+
+  // stage the gates and presence of this block's (token, slot) cells
+  for (int i = tid; i < tokens_per_block * k; i += kThreads) {
+    const int64_t t = tok0 + i / k;
+    bool here = false;
+    float g = 0.0f;
+    if (t < n_tokens && (valid == nullptr || valid[t] != 0) && row_of_entry[t * k + i % k] >= 0) {
+      here = true;
+      g = Elem<DT>::to_f32(gate[t * k + i % k]);
+    }
+    s_gate[i] = g;
+    s_here[i] = here;
+  }
+  __syncthreads();
+  const int64_t t = tok0 + local_tok;
+  if (local_tok >= tokens_per_block || t >= n_tokens) return;
+
+  float acc[EPC];
+#pragma unroll
+  for (int q = 0; q < EPC; ++q) acc[q] = 0.0f;
+  const T* ybase = y + (t * k) * hidden + c * EPC;
+#pragma unroll 8
+  for (int s = 0; s < k; ++s) {
+    if (!s_here[local_tok * k + s]) continue;           // cell computed elsewhere / invalid token
+    const float g = s_gate[local_tok * k + s];
+    const u32x4 v = *reinterpret_cast<const u32x4*>(ybase + static_cast<int64_t>(s) * hidden);
+    if constexpr (DT == MEP_DTYPE_BF16) {
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        acc[2 * q] += g * bf16_to_f32(static_cast<uint16_t>(w[q] & 0xffffu));
+        acc[2 * q + 1] += g * bf16_to_f32(static_cast<uint16_t>(w[q] >> 16));
+      }
+    } else {
+      acc[0] += g * __uint_as_float(v.x);
+      acc[1] += g * __uint_as_float(v.y);
+      acc[2] += g * __uint_as_float(v.z);
+      acc[3] += g * __uint_as_float(v.w);
+    }
+  }
+  u32x4 o;
+  if constexpr (DT == MEP_DTYPE_BF16) {
+    o.x = pack_bf16x2(acc[0], acc[1]);
+    o.y = pack_bf16x2(acc[2], acc[3]);
+    o.z = pack_bf16x2(acc[4], acc[5]);
+    o.w = pack_bf16x2(acc[6], acc[7]);
+  } else {
+    o.x = __float_as_uint(acc[0]);
+    o.y = __float_as_uint(acc[1]);
+    o.z = __float_as_uint(acc[2]);
+    o.w = __float_as_uint(acc[3]);
+  }
+  *reinterpret_cast<u32x4*>(out + t * hidden + c * EPC) = o;
+}
+
+}  // namespace
+}  // namespace mep
+
+using namespace mep;
+
+extern "C" int mep_combine(const void* y_entries, const void* topk_gate, const int32_t* row_of_entry,
+                           const uint8_t* valid_mask, int64_t n_tokens, int32_t top_k, int32_t hidden,
+                           int32_t dtype, void* out, void* stream) {
+  clear_error();
+  MEP_REQUIRE(dtype == MEP_DTYPE_F32 || dtype == MEP_DTYPE_BF16, MEP_ERR_INVALID_ARG,
+              "mep_combine: unknown dtype %d", dtype);
+  MEP_REQUIRE(n_tokens >= 0 && top_k >= 1 && top_k <= kMaxK, MEP_ERR_INVALID_ARG,
+              "mep_combine: bad n_tokens / top_k %d", top_k);
+  const int epc = 16 / dtype_bytes(dtype);
+  MEP_REQUIRE(hidden > 0 && hidden % epc == 0 && hidden / epc <= kThreads &&
+                  kThreads % (hidden / epc) == 0,
+              MEP_ERR_UNSUPPORTED, "mep_combine: hidden %d unsupported for this dtype", hidden);
+  MEP_REQUIRE(kThreads / (hidden / epc) * top_k <= kStage, MEP_ERR_UNSUPPORTED,
+              "mep_combine: hidden %d too small for top_k %d", hidden, top_k);
+  if (n_tokens == 0) return MEP_OK;
+  MEP_REQUIRE(y_entries && topk_gate && row_of_entry && out, MEP_ERR_INVALID_ARG,
+              "mep_combine: null pointer");
+  MEP_REQUIRE((reinterpret_cast<uintptr_t>(y_entries) | reinterpret_cast<uintptr_t>(out)) % 16 == 0,
+              MEP_ERR_INVALID_ARG, "mep_combine: y_entries / out must be 16-byte aligned");
+  const int tokens_per_block = kThreads / (hidden / epc);
+  const dim3 grid(static_cast<unsigned>((n_tokens + tokens_per_block - 1) / tokens_per_block));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == MEP_DTYPE_BF16)
+    combine_kernel<MEP_DTYPE_BF16><<<grid, kThreads, 0, s>>>(
+        static_cast<const uint16_t*>(y_entries), static_cast<const uint16_t*>(topk_gate), row_of_entry,
+        valid_mask, n_tokens, top_k, hidden, static_cast<uint16_t*>(out));
+  else
+    combine_kernel<MEP_DTYPE_F32><<<grid, kThreads, 0, s>>>(
+        static_cast<const float*>(y_entries), static_cast<const float*>(topk_gate), row_of_entry,
+        valid_mask, n_tokens, top_k, hidden, static_cast<float*>(out));
+  MEP_CHECK_LAUNCH("mep_combine");
+  return MEP_OK;
+}

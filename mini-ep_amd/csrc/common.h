@@ -1,0 +1,82 @@
+// Shared helpers for the gfx950 MoE kernels: bf16 conversion, MFMA operand
+// types, error reporting for the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdarg.h>
+
+#include "../../include/miniep_amd.h"
+
+namespace mep {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+// 16-byte vector used for every 128-bit load / store (a native clang vector, so
+// arrays of it stay in registers; HIP's struct-based uint4 does not always)
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------- bf16 ----
+// bf16 is carried as its raw 16-bit pattern.  Conversion to float is exact;
+// conversion from float rounds to nearest even (NaN -> quiet NaN), which is
+// what torch's .to(torch.bfloat16) does.
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+}
+
+// Element traits: storage type and conversions for the two supported dtypes.
+template <int DT> struct Elem;
+template <> struct Elem<MEP_DTYPE_F32> {
+  typedef float T;
+  static constexpr int kBytes = 4;
+  __device__ static float load(const float* p) { return *p; }
+  __device__ static float to_f32(float v) { return v; }
+  __device__ static float from_f32(float v) { return v; }
+};
+template <> struct Elem<MEP_DTYPE_BF16> {
+  typedef uint16_t T;
+  static constexpr int kBytes = 2;
+  __device__ static float to_f32(uint16_t v) { return bf16_to_f32(v); }
+  __device__ static uint16_t from_f32(float v) { return f32_to_bf16(v); }
+};
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+
+// ------------------------------------------------------------ host side ----
+void set_error(const char* fmt, ...);
+void clear_error();
+
+inline int dtype_bytes(int dtype) {
+  return dtype == MEP_DTYPE_F32 ? 4 : (dtype == MEP_DTYPE_BF16 ? 2 : 0);
+}
+
+}  // namespace mep
+
+// Report a failed precondition from a C-ABI entry point.
+#define MEP_REQUIRE(cond, code, ...)          \
+  do {                                        \
+    if (!(cond)) {                            \
+      ::mep::set_error(__VA_ARGS__);          \
+      return (code);                          \
+    }                                         \
+  } while (0)
+
+// Check the launch that was just enqueued.
+#define MEP_CHECK_LAUNCH(what)                                                   \
+  do {                                                                           \
+    hipError_t _e = hipGetLastError();                                           \
+    if (_e != hipSuccess) {                                                      \
+      ::mep::set_error("%s: launch failed: %s", (what), hipGetErrorString(_e));  \
+      return MEP_ERR_HIP;                                                        \
+    }                                                                            \
+  } while (0)

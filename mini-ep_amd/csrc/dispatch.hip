@@ -1,0 +1,401 @@
+// Dispatch for the MoE block: one GPU's share of the routed entries, stably
+// grouped by local expert, with the balancer's replica round-robin.
+//
+// Reference semantics (restated):
+//   flatten_topk (modeling.py:107-117): entry f = t*k + s, invalid tokens dropped.
+//   Placement.dest_ranks (ep.py:76-96): the w-th occurrence (flat order) of
+//     expert e inside one source's batch goes to table[e, (rr[e] + w) % n_rep[e]];
+//     afterwards rr[e] += count[e].  Layers without replicas use table[e, 0]
+//     and leave rr alone.
+//   EPMoEBackend (ep.py:216-231): route_counts += bincount; entries for this
+//     rank are received source by source in flat order, mapped through g2l
+//     (non-resident -> assert), then run_experts sorts them stably by local
+//     expert (modeling.py:94-96).
+//
+// Because everything above is a function of each entry's occurrence index w
+// inside (source segment, expert), the whole share is a closed form:
+//   kept(f)  <=>  table[e, slot(w)] == my_rank
+//   row(f)   =  offsets[g2l[e]] + sum_{s' < s} kept_in_segment(s', e)
+//               + #{w' < w : table[e, slot(w')] == my_rank}
+// and #{w' < w : (rr + w') % R == j} = (w > c) ? (w - c - 1) / R + 1 : 0 with
+// c = (j - rr) mod R.  No atomics decide any position, so the permutation is
+// bit-identical to the reference's stable sorts on every run.
+//
+// Two launches over blocks of kChunk consecutive entries of one segment:
+//   count_kernel    per-block per-expert histogram (LDS atomics; counts only)
+//   scatter_kernel  every block re-derives the prefix of its segment and the
+//                   segment totals from the histograms (nb x E ints from L2),
+//                   then ranks its entries in flat order with wave ballots and
+//                   writes perm / row_of_entry / dest.  Block 0 also writes
+//                   counts, offsets, route_counts and the updated rr.
+#include "common.h"
+
+namespace mep {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kChunk = 1024;          // entries per block
+constexpr int kMaxSeg = 16;
+constexpr int kMaxExperts = 256;
+
+struct DispatchParams {
+  const int64_t* topk_idx;
+  const uint8_t* valid;
+  int64_t n_tokens;
+  int k, E;
+  const int32_t* table;
+  const int32_t* n_rep;
+  int rmax, has_rep;
+  int64_t* rr;
+  int my_rank;
+  const int32_t* g2l;
+  int n_local;
+  int32_t* counts;
+  int32_t* offsets;
+  int32_t* perm;
+  int32_t* row_of_entry;
+  int32_t* dest;
+  int64_t* route_counts;
+  // workspace
+  uint32_t* header;     // [0] = number of launched blocks
+  uint32_t* flags;      // [2 * nbl]: count-kernel flags, scatter-kernel flags
+  int64_t* rr_snap;     // [S * E]
+  int32_t* bc;          // [nbl * E]
+  int nb, nbl, n_seg;
+  int64_t seg_entry[kMaxSeg + 1];
+  int seg_block[kMaxSeg + 1];
+};
+
+enum : uint32_t { kFlagRange = 1u, kFlagResident = 2u };
+
+__device__ __forceinline__ int segment_of_block(const DispatchParams& p, int b) {
+  int s = 0;
+  for (int i = 0; i < p.n_seg; ++i)
+    if (b >= p.seg_block[i] && b < p.seg_block[i + 1]) s = i;
+  return s;
+}
+
+__device__ __forceinline__ void block_range(const DispatchParams& p, int b, int s, int64_t& f0,
+                                            int64_t& f1) {
+  if (b >= p.nb) { f0 = f1 = 0; return; }
+  f0 = p.seg_entry[s] + static_cast<int64_t>(b - p.seg_block[s]) * kChunk;
+  f1 = f0 + kChunk;
+  if (f1 > p.seg_entry[s + 1]) f1 = p.seg_entry[s + 1];
+}
+
+// Replica count of e clamped to the table width (keeps every table read in bounds).
+__device__ __forceinline__ int reps(const DispatchParams& p, int e) {
+  const int r = p.n_rep[e];
+  return r < 1 ? 1 : (r > p.rmax ? p.rmax : r);
+}
+
+// #{w' in [0, w) : (rr + w') mod R == j}, summed over the slots j this rank holds.
+
+__device__ __forceinline__ int64_t kept_before(const DispatchParams& p, int e, int64_t w, int64_t rr) {
+  const int R = reps(p, e);
+  int64_t n = 0;
+  const int64_t rmod = rr % R;
+  for (int j = 0; j < R; ++j) {
+    if (p.table[e * p.rmax + j] != p.my_rank) continue;
+    const int64_t c = ((j - rmod) % R + R) % R;
+    if (w > c) n += (w - c - 1) / R + 1;
+  }
+  return n;
+}
+
+__global__ __launch_bounds__(kThreads) void count_kernel(DispatchParams p) {
+  __shared__ int cnt[kMaxExperts];
+  __shared__ uint32_t flag;
+  const int b = blockIdx.x, tid = threadIdx.x;
+  for (int e = tid; e < p.E; e += kThreads) cnt[e] = 0;
+  if (tid == 0) flag = 0;
+  __syncthreads();
+  const int s = segment_of_block(p, b);
+  int64_t f0, f1;
+  block_range(p, b, s, f0, f1);
+  for (int64_t f = f0 + tid; f < f1; f += kThreads) {
+    const int64_t t = f / p.k;
+    if (p.valid != nullptr && p.valid[t] == 0) continue;
+    const int64_t e = p.topk_idx[f];
+    if (e < 0 || e >= p.E) { atomicOr(&flag, kFlagRange); continue; }
+    atomicAdd(&cnt[e], 1);
+  }
+  __syncthreads();
+  for (int e = tid; e < p.E; e += kThreads) p.bc[static_cast<int64_t>(b) * p.E + e] = cnt[e];
+  if (tid == 0) p.flags[b] = flag;
+  if (b == 0) {
+    if (tid == 0) p.header[0] = static_cast<uint32_t>(p.nbl);
+    if (p.has_rep)
+      for (int i = tid; i < p.n_seg * p.E; i += kThreads) p.rr_snap[i] = p.rr[i];
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void scatter_kernel(DispatchParams p) {
+  __shared__ int segtot[kMaxSeg][kMaxExperts];   // entries of expert e in segment s
+  __shared__ int pre[kMaxExperts];                // ... in earlier blocks of my segment
+  __shared__ int keptbase[kMaxExperts];           // kept entries of e in earlier segments
+  __shared__ int loff[kMaxExperts];               // first row of e's local expert
+  __shared__ int lcount[kMaxExperts];             // rows per local expert
+  __shared__ int run[kMaxExperts];                // entries of e seen in earlier rounds
+  __shared__ int wcnt[kThreads / 64][kMaxExperts + 1];
+  __shared__ uint32_t flag;
+
+  const int b = blockIdx.x, tid = threadIdx.x;
+  const int E = p.E;
+  const int s = segment_of_block(p, b);
+  int64_t f0, f1;
+  block_range(p, b, s, f0, f1);
+
+  for (int i = tid; i < p.n_seg * kMaxExperts; i += kThreads) segtot[i / kMaxExperts][i % kMaxExperts] = 0;
+  for (int e = tid; e < E; e += kThreads) { pre[e] = 0; run[e] = 0; lcount[e] = 0; }
+  for (int i = tid; i < (kThreads / 64) * (kMaxExperts + 1); i += kThreads)
+    wcnt[i / (kMaxExperts + 1)][i % (kMaxExperts + 1)] = 0;
+  if (tid == 0) flag = 0;
+  __syncthreads();
+
+  // 1. segment totals and my prefix, from the per-block histograms
+  {
+    const int parts = kThreads / E > 0 ? kThreads / E : 1;
+    const int e = tid % E, part = tid / E;
+    if (part < parts && tid < parts * E) {
+      int my_pre = 0;
+      for (int bb = part; bb < p.nb; bb += parts) {
+        const int c = p.bc[static_cast<int64_t>(bb) * E + e];
+        const int sb = segment_of_block(p, bb);
+        atomicAdd(&segtot[sb][e], c);
+        if (sb == s && bb < b) my_pre += c;
+      }
+      atomicAdd(&pre[e], my_pre);
+    }
+  }
+  __syncthreads();
+
+  // 2. kept entries per (segment, expert) -> local counts and my segment base
+  for (int e = tid; e < E; e += kThreads) {
+    int64_t total = 0, base = 0;
+    for (int sg = 0; sg < p.n_seg; ++sg) {
+      int64_t kept;
+      if (p.has_rep) kept = kept_before(p, e, segtot[sg][e], p.rr_snap[sg * E + e]);
+      else kept = (p.table[e * p.rmax] == p.my_rank) ? segtot[sg][e] : 0;
+      if (sg < s) base += kept;
+      total += kept;
+    }
+    keptbase[e] = static_cast<int>(base);
+    const int j = p.g2l[e];
+    if (j >= 0 && j < p.n_local) lcount[j] = static_cast<int>(total);
+  }
+  __syncthreads();
+  for (int e = tid; e < E; e += kThreads) {
+    const int j = p.g2l[e];
+    int off = 0;
+    if (j >= 0 && j < p.n_local)
+      for (int jj = 0; jj < j; ++jj) off += lcount[jj];
+    loff[e] = off;
+  }
+  if (b == 0) {
+    for (int j = tid; j <= p.n_local; j += kThreads) {
+      int off = 0;
+      for (int jj = 0; jj < j; ++jj) off += lcount[jj];
+      p.offsets[j] = off;
+      if (j < p.n_local) p.counts[j] = lcount[j];
+    }
+    for (int e = tid; e < E; e += kThreads) {
+      int64_t tot = 0;
+      for (int sg = 0; sg < p.n_seg; ++sg) {
+        tot += segtot[sg][e];
+        if (p.has_rep) p.rr[sg * E + e] = p.rr_snap[sg * E + e] + segtot[sg][e];
+      }
+      if (p.route_counts != nullptr) p.route_counts[e] += tot;
+    }
+  }
+  __syncthreads();
+
+  // 3. rank this block's entries in flat order and scatter
+  const int lane = tid & 63, wave = tid >> 6;
+  const int nbits = 32 - __clz(E);
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  for (int64_t base_f = f0; base_f < f1; base_f += kThreads) {
+    const int64_t f = base_f + tid;
+    int key = E;
+    if (f < f1) {
+      const int64_t t = f / p.k;
+      const bool valid = p.valid == nullptr || p.valid[t] != 0;
+      const int64_t e = p.topk_idx[f];
+      if (valid && e >= 0 && e < E) {
+        key = static_cast<int>(e);
+      } else {
+        p.row_of_entry[f] = -1;
+        if (p.dest != nullptr) p.dest[f] = -1;
+      }
+    }
+    uint64_t peers = ~0ull;
+    for (int bit = 0; bit < nbits; ++bit) {
+      const bool on = (key >> bit) & 1;
+      const uint64_t m = __ballot(on);
+      peers &= on ? m : ~m;
+    }
+    const int rank_w = __popcll(peers & lt_mask);
+    if (key < E && rank_w == 0) wcnt[wave][key] = __popcll(peers);
+    __syncthreads();
+    if (key < E) {
+      int w = pre[key] + run[key] + rank_w;
+      for (int ww = 0; ww < wave; ++ww) w += wcnt[ww][key];
+      const int e = key;
+      const int64_t rr0 = p.has_rep ? p.rr_snap[s * E + e] : 0;
+      const int R = reps(p, e);
+      // floor modulo, as torch's % on int64 tensors (ep.py:94)
+      const int slot = p.has_rep ? static_cast<int>(((rr0 + w) % R + R) % R) : 0;
+      const int d = p.table[e * p.rmax + slot];
+      if (p.dest != nullptr) p.dest[f] = d;
+      int row = -1;
+      if (d == p.my_rank) {
+        const int j = p.g2l[e];
+        if (j >= 0 && j < p.n_local) {
+          const int64_t kb = p.has_rep ? kept_before(p, e, w, rr0) : w;
+          row = loff[e] + keptbase[e] + static_cast<int>(kb);
+          p.perm[row] = static_cast<int32_t>(f);
+        } else {
+          atomicOr(&flag, kFlagResident);
+        }
+      }
+      p.row_of_entry[f] = row;
+    }
+    __syncthreads();
+    for (int e = tid; e < E; e += kThreads) {
+      int add = 0;
+      for (int ww = 0; ww < kThreads / 64; ++ww) { add += wcnt[ww][e]; wcnt[ww][e] = 0; }
+      run[e] += add;
+    }
+    __syncthreads();
+  }
+  if (tid == 0) p.flags[p.nbl + b] = flag;
+}
+
+size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+struct WsLayout {
+  size_t header, flags, rr_snap, bc, total;
+};
+
+WsLayout ws_layout(int nbl, int n_seg, int E) {
+  WsLayout l;
+  l.header = 0;
+  l.flags = 256;
+  l.rr_snap = align_up(l.flags + sizeof(uint32_t) * 2 * nbl, 256);
+  l.bc = align_up(l.rr_snap + sizeof(int64_t) * n_seg * E, 256);
+  l.total = align_up(l.bc + sizeof(int32_t) * static_cast<size_t>(nbl) * E, 256);
+  return l;
+}
+
+int count_blocks(const int64_t* seg_tokens, int n_seg, int k, int* seg_block) {
+  int nb = 0;
+  for (int s = 0; s < n_seg; ++s) {
+    seg_block[s] = nb;
+    const int64_t ne = (seg_tokens[s + 1] - seg_tokens[s]) * k;
+    nb += static_cast<int>((ne + kChunk - 1) / kChunk);
+  }
+  seg_block[n_seg] = nb;
+  return nb;
+}
+
+}  // namespace
+}  // namespace mep
+
+using namespace mep;
+
+extern "C" size_t mep_dispatch_workspace_size(int64_t n_tokens, int32_t top_k, int32_t n_experts,
+                                              int32_t n_segments, const int64_t* seg_tokens) {
+  int64_t one_seg[2] = {0, n_tokens};
+  if (n_segments <= 0 || seg_tokens == nullptr) { n_segments = 1; seg_tokens = one_seg; }
+  if (n_segments > kMaxSeg || top_k <= 0 || n_experts <= 0) return 0;
+  int seg_block[kMaxSeg + 1];
+  const int nb = count_blocks(seg_tokens, n_segments, top_k, seg_block);
+  return ws_layout(nb > 0 ? nb : 1, n_segments, n_experts).total;
+}
+
+extern "C" int mep_dispatch(const int64_t* topk_idx, const uint8_t* valid_mask, int64_t n_tokens,
+                            int32_t top_k, int32_t n_experts, const int32_t* table,
+                            const int32_t* n_rep, int32_t rmax, int32_t has_replicas, int64_t* rr,
+                            const int64_t* seg_tokens, int32_t n_segments, int32_t my_rank,
+                            const int32_t* g2l, int32_t n_local, int32_t* counts, int32_t* offsets,
+                            int32_t* perm, int32_t* row_of_entry, int32_t* dest,
+                            int64_t* route_counts, void* workspace, size_t workspace_bytes,
+                            void* stream) {
+  clear_error();
+  MEP_REQUIRE(n_tokens >= 0 && top_k >= 1 && top_k <= 32, MEP_ERR_INVALID_ARG,
+              "mep_dispatch: bad n_tokens %lld / top_k %d", (long long)n_tokens, top_k);
+  MEP_REQUIRE(n_experts >= 1 && n_experts <= kMaxExperts, MEP_ERR_UNSUPPORTED,
+              "mep_dispatch: n_experts %d outside [1, %d]", n_experts, kMaxExperts);
+  MEP_REQUIRE(n_tokens * top_k < (int64_t(1) << 31), MEP_ERR_UNSUPPORTED,
+              "mep_dispatch: n_tokens * top_k must be < 2^31");
+  MEP_REQUIRE(rmax >= 1, MEP_ERR_INVALID_ARG, "mep_dispatch: rmax %d < 1", rmax);
+  MEP_REQUIRE(n_local >= 0 && n_local <= n_experts, MEP_ERR_INVALID_ARG,
+              "mep_dispatch: n_local %d outside [0, %d]", n_local, n_experts);
+  MEP_REQUIRE(n_segments >= 1 && n_segments <= kMaxSeg && seg_tokens != nullptr,
+              MEP_ERR_INVALID_ARG, "mep_dispatch: need 1..%d segments (got %d)", kMaxSeg, n_segments);
+  MEP_REQUIRE(seg_tokens[0] == 0 && seg_tokens[n_segments] == n_tokens, MEP_ERR_INVALID_ARG,
+              "mep_dispatch: seg_tokens must run from 0 to n_tokens");
+  for (int s = 0; s < n_segments; ++s)
+    MEP_REQUIRE(seg_tokens[s + 1] >= seg_tokens[s], MEP_ERR_INVALID_ARG,
+                "mep_dispatch: seg_tokens must be non-decreasing");
+  MEP_REQUIRE(topk_idx || n_tokens == 0, MEP_ERR_INVALID_ARG, "mep_dispatch: topk_idx is null");
+  MEP_REQUIRE(table && n_rep && g2l && offsets && workspace, MEP_ERR_INVALID_ARG,
+              "mep_dispatch: null table / n_rep / g2l / offsets / workspace");
+  MEP_REQUIRE((counts && perm && row_of_entry) || n_tokens == 0 || n_local == 0, MEP_ERR_INVALID_ARG,
+              "mep_dispatch: null counts / perm / row_of_entry");
+  MEP_REQUIRE(!has_replicas || rr != nullptr, MEP_ERR_INVALID_ARG,
+              "mep_dispatch: rr is required when the layer has replicas");
+
+  DispatchParams p;
+  p.nb = count_blocks(seg_tokens, n_segments, top_k, p.seg_block);
+  p.nbl = p.nb > 0 ? p.nb : 1;
+  const WsLayout l = ws_layout(p.nbl, n_segments, n_experts);
+  MEP_REQUIRE(workspace_bytes >= l.total, MEP_ERR_WORKSPACE,
+              "mep_dispatch: workspace %zu B < required %zu B", workspace_bytes, l.total);
+  char* ws = static_cast<char*>(workspace);
+  p.topk_idx = topk_idx; p.valid = valid_mask; p.n_tokens = n_tokens;
+  p.k = top_k; p.E = n_experts; p.table = table; p.n_rep = n_rep; p.rmax = rmax;
+  p.has_rep = has_replicas ? 1 : 0; p.rr = rr; p.my_rank = my_rank; p.g2l = g2l;
+  p.n_local = n_local; p.counts = counts; p.offsets = offsets; p.perm = perm;
+  p.row_of_entry = row_of_entry; p.dest = dest; p.route_counts = route_counts;
+  p.header = reinterpret_cast<uint32_t*>(ws + l.header);
+  p.flags = reinterpret_cast<uint32_t*>(ws + l.flags);
+  p.rr_snap = reinterpret_cast<int64_t*>(ws + l.rr_snap);
+  p.bc = reinterpret_cast<int32_t*>(ws + l.bc);
+  p.n_seg = n_segments;
+  for (int s = 0; s <= n_segments; ++s) p.seg_entry[s] = seg_tokens[s] * top_k;
+  for (int s = n_segments + 1; s <= kMaxSeg; ++s) { p.seg_entry[s] = p.seg_entry[n_segments]; p.seg_block[s] = p.nb; }
+
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  count_kernel<<<p.nbl, kThreads, 0, st>>>(p);
+  MEP_CHECK_LAUNCH("mep_dispatch(count)");
+  scatter_kernel<<<p.nbl, kThreads, 0, st>>>(p);
+  MEP_CHECK_LAUNCH("mep_dispatch(scatter)");
+  return MEP_OK;
+}
+
+extern "C" int mep_dispatch_check(const void* workspace, void* stream) {
+  clear_error();
+  MEP_REQUIRE(workspace != nullptr, MEP_ERR_INVALID_ARG, "mep_dispatch_check: null workspace");
+  hipError_t e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
+  MEP_REQUIRE(e == hipSuccess, MEP_ERR_HIP, "mep_dispatch_check: %s", hipGetErrorString(e));
+  uint32_t nbl = 0;
+  e = hipMemcpy(&nbl, workspace, sizeof(nbl), hipMemcpyDeviceToHost);
+  MEP_REQUIRE(e == hipSuccess, MEP_ERR_HIP, "mep_dispatch_check: %s", hipGetErrorString(e));
+  MEP_REQUIRE(nbl >= 1 && nbl < (1u << 24), MEP_ERR_INVALID_ARG,
+              "mep_dispatch_check: workspace holds no dispatch result");
+  uint32_t acc = 0;
+  uint32_t buf[1024];
+  const char* flags = static_cast<const char*>(workspace) + 256;
+  for (uint32_t i = 0; i < 2 * nbl; i += 1024) {
+    const uint32_t n = (2 * nbl - i) < 1024 ? (2 * nbl - i) : 1024;
+    e = hipMemcpy(buf, flags + sizeof(uint32_t) * i, sizeof(uint32_t) * n, hipMemcpyDeviceToHost);
+    MEP_REQUIRE(e == hipSuccess, MEP_ERR_HIP, "mep_dispatch_check: %s", hipGetErrorString(e));
+    for (uint32_t j = 0; j < n; ++j) acc |= buf[j];
+  }
+  MEP_REQUIRE(!(acc & kFlagRange), MEP_ERR_EXPERT_RANGE,
+              "mep_dispatch: expert id outside [0, n_experts) dropped");
+  MEP_REQUIRE(!(acc & kFlagResident), MEP_ERR_NOT_RESIDENT,
+              "mep_dispatch: entry routed to this rank for a non-resident expert dropped");
+  return MEP_OK;
+}

@@ -1,0 +1,260 @@
+"""Tensor-level wrappers of the HIP kernels (device tensors in, device tensors out).
+
+Every function here enqueues work on torch's current HIP stream through the
+C ABI and returns without synchronising (except ``dispatch(check=True)``,
+which mirrors the residency assert of miniep/ep.py:230).  There is no CPU
+path: CPU tensors are rejected.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+
+_DTYPES = {torch.float32: _lib.DTYPE_F32, torch.bfloat16: _lib.DTYPE_BF16}
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    try:
+        return _DTYPES[t.dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {t.dtype}; the kernels take float32 or bfloat16") from None
+
+
+def _require_device(*tensors: torch.Tensor) -> torch.device:
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise RuntimeError("the MoE kernels run on the GPU only; got a CPU tensor")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"tensors on different devices: {dev} vs {t.device}")
+    return dev
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _mask_u8(valid_mask: torch.Tensor | None, n: int) -> torch.Tensor | None:
+    if valid_mask is None:
+        return None
+    vm = valid_mask.reshape(-1)
+    if vm.numel() != n:
+        raise ValueError(f"valid_mask has {vm.numel()} entries, expected {n}")
+    return vm.to(torch.uint8).contiguous()
+
+
+# ----------------------------------------------------------------------------
+# router (modeling.py:192-195)
+# ----------------------------------------------------------------------------
+def router_topk(x_flat: torch.Tensor, w_router: torch.Tensor, k: int, return_logits: bool = False):
+    """topk_idx (N,k) int64, topk_gate (N,k) x.dtype [, logits (N,E) fp32].
+
+    logits = x_flat @ w_router.T accumulated in fp32; topk descending with
+    equal logits resolved to the lower expert id; gate = fp32 softmax of the
+    k selected logits stored in x.dtype (modeling.py:193-195)."""
+    dev = _require_device(x_flat, w_router)
+    x = x_flat.contiguous()
+    w = w_router.to(x.dtype).contiguous()
+    n, h = x.shape
+    e = w.shape[0]
+    if w.shape[1] != h:
+        raise ValueError(f"router weight {tuple(w.shape)} does not match hidden {h}")
+    idx = torch.empty((n, k), dtype=torch.int64, device=dev)
+    gate = torch.empty((n, k), dtype=x.dtype, device=dev)
+    logits = torch.empty((n, e), dtype=torch.float32, device=dev) if return_logits else None
+    rc = _lib.lib().mep_router_topk(x.data_ptr(), w.data_ptr(), n, h, e, k, _dtype_code(x),
+                                    idx.data_ptr(), gate.data_ptr(), _ptr(logits), _stream(dev))
+    _lib.check(rc, "mep_router_topk")
+    return (idx, gate, logits) if return_logits else (idx, gate)
+
+
+def topk_softmax(logits: torch.Tensor, k: int, gate_dtype: torch.dtype = torch.float32):
+    """Top-k + fp32 softmax of precomputed fp32 logits (modeling.py:194-195)."""
+    dev = _require_device(logits)
+    lg = logits.to(torch.float32).contiguous()
+    n, e = lg.shape
+    idx = torch.empty((n, k), dtype=torch.int64, device=dev)
+    gate = torch.empty((n, k), dtype=gate_dtype, device=dev)
+    code = _DTYPES[gate_dtype]
+    rc = _lib.lib().mep_topk_softmax(lg.data_ptr(), n, e, k, code, idx.data_ptr(), gate.data_ptr(),
+                                     _stream(dev))
+    _lib.check(rc, "mep_topk_softmax")
+    return idx, gate
+
+
+# ----------------------------------------------------------------------------
+# dispatch (modeling.py:94-96,107-117; ep.py:76-96,216-231)
+# ----------------------------------------------------------------------------
+@dataclass
+class Dispatch:
+    """One GPU's share of a routed batch, grouped by local expert.
+
+    counts (n_local,) / offsets (n_local+1,) int32 rows per local expert;
+    perm (N*k,) int32 flat entry id of each row (first offsets[-1] valid);
+    row_of_entry (N*k,) int32 row of each entry here or -1; dest (N*k,) int32
+    destination rank or -1 (only when requested)."""
+    counts: torch.Tensor
+    offsets: torch.Tensor
+    perm: torch.Tensor
+    row_of_entry: torch.Tensor
+    dest: torch.Tensor | None
+    n_tokens: int
+    top_k: int
+    n_local: int
+
+    @property
+    def max_rows(self) -> int:
+        return self.n_tokens * self.top_k
+
+
+def dispatch(topk_idx: torch.Tensor, valid_mask: torch.Tensor | None, n_experts: int,
+             table: torch.Tensor, n_rep: torch.Tensor, has_replicas: bool,
+             rr: torch.Tensor | None, my_rank: int, g2l: torch.Tensor, n_local: int,
+             seg_tokens=None, route_counts: torch.Tensor | None = None,
+             want_dest: bool = False, check: bool = True) -> Dispatch:
+    """Run mep_dispatch.  ``table`` (E,Rmax) / ``n_rep`` (E,) / ``g2l`` (E,) are
+    int32 device tensors; ``rr`` is the (S,E) int64 device counter block
+    (updated in place when ``has_replicas``); ``seg_tokens`` the S+1 token
+    offsets of the source segments (default: one segment)."""
+    dev = _require_device(topk_idx, table, n_rep, g2l, rr, route_counts)
+    idx = topk_idx.to(torch.int64).contiguous()
+    n, k = idx.shape
+    if seg_tokens is None:
+        seg_tokens = [0, n]
+    seg = [int(v) for v in seg_tokens]
+    n_seg = len(seg) - 1
+    seg_arr = (ctypes.c_int64 * len(seg))(*seg)
+    vm = _mask_u8(valid_mask, n)
+    for name, t, dt in (("table", table, torch.int32), ("n_rep", n_rep, torch.int32),
+                        ("g2l", g2l, torch.int32)):
+        if t.dtype != dt or not t.is_contiguous():
+            raise TypeError(f"{name} must be a contiguous {dt} tensor")
+    if rr is not None and (rr.dtype != torch.int64 or not rr.is_contiguous() or rr.numel() != n_seg * n_experts):
+        raise TypeError(f"rr must be a contiguous int64 tensor of {n_seg}x{n_experts}")
+    if route_counts is not None and (route_counts.dtype != torch.int64 or route_counts.numel() != n_experts):
+        raise TypeError("route_counts must be an int64 tensor of n_experts")
+    L = _lib.lib()
+    ws_bytes = L.mep_dispatch_workspace_size(n, k, n_experts, n_seg, seg_arr)
+    ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
+    nk = max(n * k, 1)
+    counts = torch.empty(max(n_local, 1), dtype=torch.int32, device=dev)
+    offsets = torch.empty(n_local + 1, dtype=torch.int32, device=dev)
+    perm = torch.empty(nk, dtype=torch.int32, device=dev)
+    row_of_entry = torch.empty(nk, dtype=torch.int32, device=dev)
+    dest = torch.empty(nk, dtype=torch.int32, device=dev) if want_dest else None
+    st = _stream(dev)
+    rc = L.mep_dispatch(_ptr(idx), _ptr(vm), n, k, n_experts, table.data_ptr(), n_rep.data_ptr(),
+                        table.shape[1], 1 if has_replicas else 0, _ptr(rr), seg_arr, n_seg,
+                        my_rank, g2l.data_ptr(), n_local, counts.data_ptr(), offsets.data_ptr(),
+                        perm.data_ptr(), row_of_entry.data_ptr(), _ptr(dest), _ptr(route_counts),
+                        ws.data_ptr(), ws.numel(), st)
+    _lib.check(rc, "mep_dispatch")
+    if check:
+        _lib.check(L.mep_dispatch_check(ws.data_ptr(), st), "mep_dispatch")
+    return Dispatch(counts[:n_local], offsets, perm, row_of_entry, dest, n, k, n_local)
+
+
+# ----------------------------------------------------------------------------
+# grouped SwiGLU experts (modeling.py:83-104) and combine (modeling.py:120-128,144)
+# ----------------------------------------------------------------------------
+def grouped_swiglu(x_flat: torch.Tensor, disp: Dispatch, w_in: torch.Tensor, w_out: torch.Tensor,
+                   y_entries: torch.Tensor | None = None) -> torch.Tensor:
+    """Expert outputs for every dispatched row, written to the row's
+    (token, slot) cell of ``y_entries`` (N*k, H) (allocated if not given)."""
+    dev = _require_device(x_flat, w_in, w_out, y_entries)
+    x = x_flat.contiguous()
+    n, h = x.shape
+    if w_in.dim() != 3 or w_out.dim() != 3:
+        raise ValueError("w_in must be (E, 2I, H) and w_out (E, H, I)")
+    e_loc, two_i, h_in = w_in.shape
+    inter = two_i // 2
+    if h_in != h or tuple(w_out.shape) != (e_loc, h, inter) or e_loc != disp.n_local:
+        raise ValueError(f"weight shapes {tuple(w_in.shape)} / {tuple(w_out.shape)} do not match "
+                         f"hidden {h} and {disp.n_local} local experts")
+    wi = w_in.to(x.dtype).contiguous()
+    wo = w_out.to(x.dtype).contiguous()
+    if y_entries is None:
+        y_entries = torch.empty((max(n * disp.top_k, 1), h), dtype=x.dtype, device=dev)
+    code = _dtype_code(x)
+    L = _lib.lib()
+    max_rows = n * disp.top_k
+    ws_bytes = L.mep_experts_workspace_size(max_rows, inter, code)
+    ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
+    rc = L.mep_grouped_swiglu(x.data_ptr(), n, disp.top_k, disp.perm.data_ptr(), disp.offsets.data_ptr(),
+                              disp.n_local, max_rows, wi.data_ptr(), wo.data_ptr(), h, inter, code,
+                              y_entries.data_ptr(), ws.data_ptr(), ws.numel(), _stream(dev))
+    _lib.check(rc, "mep_grouped_swiglu")
+    return y_entries
+
+
+def _expert_shapes(x, disp, w_in=None, w_out=None):
+    n, h = x.shape
+    if w_in is not None:
+        e_loc, two_i, h_in = w_in.shape
+        if h_in != h or e_loc != disp.n_local:
+            raise ValueError(f"w_in {tuple(w_in.shape)} does not match hidden {h} / {disp.n_local} experts")
+        return n, h, two_i // 2
+    e_loc, h_out, inter = w_out.shape
+    if h_out != h or e_loc != disp.n_local:
+        raise ValueError(f"w_out {tuple(w_out.shape)} does not match hidden {h} / {disp.n_local} experts")
+    return n, h, inter
+
+
+def swiglu_gate_up(x_flat: torch.Tensor, disp: Dispatch, w_in: torch.Tensor,
+                   act: torch.Tensor | None = None) -> torch.Tensor:
+    """GEMM-1 + SwiGLU only: act (N*k, I) rows in dispatch order (modeling.py:101-102)."""
+    dev = _require_device(x_flat, w_in, act)
+    x = x_flat.contiguous()
+    n, h, inter = _expert_shapes(x, disp, w_in=w_in)
+    if act is None:
+        act = torch.empty((max(n * disp.top_k, 1), inter), dtype=x.dtype, device=dev)
+    wi = w_in.to(x.dtype).contiguous()
+    rc = _lib.lib().mep_swiglu_gate_up(x.data_ptr(), n, disp.top_k, disp.perm.data_ptr(),
+                                       disp.offsets.data_ptr(), disp.n_local, n * disp.top_k,
+                                       wi.data_ptr(), h, inter, _dtype_code(x), act.data_ptr(),
+                                       act.numel() * act.element_size(), _stream(dev))
+    _lib.check(rc, "mep_swiglu_gate_up")
+    return act
+
+
+def swiglu_down(act: torch.Tensor, x_flat: torch.Tensor, disp: Dispatch, w_out: torch.Tensor,
+                y_entries: torch.Tensor | None = None) -> torch.Tensor:
+    """GEMM-2 + scatter to (token, slot) cells (modeling.py:103)."""
+    dev = _require_device(act, x_flat, w_out, y_entries)
+    n, h, inter = _expert_shapes(x_flat, disp, w_out=w_out)
+    if y_entries is None:
+        y_entries = torch.empty((max(n * disp.top_k, 1), h), dtype=act.dtype, device=dev)
+    wo = w_out.to(act.dtype).contiguous()
+    rc = _lib.lib().mep_swiglu_down(act.data_ptr(), n, disp.top_k, disp.perm.data_ptr(),
+                                    disp.offsets.data_ptr(), disp.n_local, n * disp.top_k, wo.data_ptr(),
+                                    h, inter, _dtype_code(act), y_entries.data_ptr(), _stream(dev))
+    _lib.check(rc, "mep_swiglu_down")
+    return y_entries
+
+
+def combine(y_entries: torch.Tensor, topk_gate: torch.Tensor, row_of_entry: torch.Tensor,
+            valid_mask: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """out[t] = sum over present slots s (slot order) of gate[t,s] * y[t*k+s]."""
+    dev = _require_device(y_entries, topk_gate, row_of_entry, out)
+    n, k = topk_gate.shape
+    h = y_entries.shape[1]
+    gate = topk_gate.to(y_entries.dtype).contiguous()
+    vm = _mask_u8(valid_mask, n)
+    if out is None:
+        out = torch.empty((n, h), dtype=y_entries.dtype, device=dev)
+    rc = _lib.lib().mep_combine(y_entries.data_ptr(), gate.data_ptr(), row_of_entry.data_ptr(), _ptr(vm),
+                                n, k, h, _dtype_code(y_entries), out.data_ptr(), _stream(dev))
+    _lib.check(rc, "mep_combine")
+    return out

@@ -1,0 +1,36 @@
+"""Shared helpers of the GPU parity tests."""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+# tolerances of the MoE output vs the oracle:
+# max |out - ref| <= TOL * max |ref|
+TOL_F32 = 1e-5
+TOL_BF16 = 2e-2
+
+
+def rel_err(got, ref) -> float:
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    scale = np.abs(ref).max()
+    if scale == 0:
+        return float(np.abs(got).max())
+    return float(np.abs(got - ref).max() / scale)
+
+
+def to_np(t: torch.Tensor) -> np.ndarray:
+    """Device tensor -> numpy (bf16 widened to its exact float32 values)."""
+    t = t.detach()
+    if t.dtype == torch.bfloat16:
+        t = t.float()
+    return t.cpu().numpy()
+
+
+def banner(msg: str) -> None:
+    print(f"[case] {msg}", flush=True)
+
+
+def tie_free(logits: np.ndarray, k: int) -> bool:
+    s = -np.sort(-logits, axis=1)
+    return not (s[:, : k] == s[:, 1: k + 1]).any()

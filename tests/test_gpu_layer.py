@@ -1,0 +1,134 @@
+"""End-to-end MoE layer on the GPU vs the oracle: router hook + backend.
+
+The layer is what Block.forward does after its post-attention RMSNorm
+(modeling.py:190-196): route, then the backend returns the combined (N, H)
+expert output.  Configurations: fp32 T=512 (bar 1e-5), decode bf16 T=32,
+skewed bf16 T=16384 (bar 2e-2), one rank's share under the balanced plan.
+"""
+import json
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import TOL_BF16, TOL_F32, banner, rel_err, to_np
+from miniep_amd import EmulatedEPMoEBackend, HipEPShareBackend, HipMoEBackend, Placement, ops, route, workloads
+from oracle import moe_oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _layer_on_gpu(L, dtype, valid=None, check=True):
+    x = L.x.to(dtype).to(DEV)
+    backend = HipMoEBackend(L.w_in.to(dtype).to(DEV), L.w_out.to(dtype).to(DEV), check=check)
+    idx, gate, logits = route(x, L.w_router.to(dtype).to(DEV), L.top_k, return_logits=True)
+    out = backend(x, idx, gate, None if valid is None else valid.to(DEV))
+    return out, idx, gate, logits, backend
+
+
+def _oracle_layer(L, dtype, logits, valid=None, tokens=None):
+    """Oracle layer on the kernel's fp32 logits (routing bit-exact given them)."""
+    bf = dtype == torch.bfloat16
+    xr = L.x.to(dtype).float().numpy()
+    idx, gate = O.topk_softmax(logits, L.top_k, gate_bf16=bf)
+    sel = slice(None) if tokens is None else tokens
+    v = None if valid is None else valid.numpy()[sel]
+    return O.moe_layer_local(xr[sel], idx[sel], gate[sel], L.w_in.to(dtype).float().numpy(),
+                             L.w_out.to(dtype).float().numpy(), v, act_bf16=bf, out_bf16=bf), idx, gate
+
+
+def test_fp32_layer_t512():
+    banner("layer fp32 t=512")
+    L = workloads.make_layer(512, seed=0)
+    out, idx, gate, logits, _ = _layer_on_gpu(L, torch.float32)
+    ref, ridx, _ = _oracle_layer(L, torch.float32, to_np(logits))
+    assert np.array_equal(to_np(idx), ridx)
+    err = rel_err(to_np(out), ref)
+    print(f"rel err {err:.3e}")
+    assert err <= TOL_F32
+
+
+def test_decode_bf16_t32():
+    banner("layer bf16 t=32")
+    L = workloads.make_layer(32, seed=1)
+    out, idx, gate, logits, be = _layer_on_gpu(L, torch.bfloat16)
+    ref, ridx, _ = _oracle_layer(L, torch.bfloat16, to_np(logits))
+    assert np.array_equal(to_np(idx), ridx)
+    assert rel_err(to_np(out), ref) <= TOL_BF16
+    assert int(to_np(be.last_dispatch.counts).sum()) == 32 * 8
+
+
+def test_masked_tokens_and_dummy_prefill():
+    banner("layer masks")
+    L = workloads.make_layer(700, seed=2)
+    valid = torch.rand(700, generator=torch.Generator().manual_seed(0)) < 0.7
+    out, idx, gate, logits, _ = _layer_on_gpu(L, torch.bfloat16, valid)
+    ref, _, _ = _oracle_layer(L, torch.bfloat16, to_np(logits), valid)
+    o = to_np(out)
+    assert (o[~valid.numpy()] == 0).all()
+    assert rel_err(o, ref) <= TOL_BF16
+    # dummy prefill: zero expert load (worker.py:112-122)
+    out0, *_ = _layer_on_gpu(L, torch.bfloat16, torch.zeros(700, dtype=torch.bool))
+    assert (to_np(out0) == 0).all()
+
+
+def test_skewed_bf16_t16384():
+    banner("layer bf16 t=16384 zipf 1.2")
+    L = workloads.make_layer(16384, seed=0, zipf_s=1.2)
+    out, idx, gate, logits, be = _layer_on_gpu(L, torch.bfloat16, check=False)
+    lg = to_np(logits)
+    ridx, _ = O.topk_softmax(lg, 8, gate_bf16=True)
+    assert np.array_equal(to_np(idx), ridx)
+    counts = np.bincount(ridx.reshape(-1), minlength=32)
+    assert to_np(be.last_dispatch.counts).tolist() == counts.tolist()
+    toks = np.random.default_rng(0).choice(16384, 1024, replace=False)
+    ref, _, _ = _oracle_layer(L, torch.bfloat16, lg, tokens=toks)
+    err = rel_err(to_np(out)[toks], ref)
+    print(f"rel err {err:.3e}")
+    assert err <= TOL_BF16
+    # bitwise identical on a second run
+    out2 = be(L.x.to(torch.bfloat16).to(DEV), idx, gate)
+    assert torch.equal(out, out2)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_emulated_ep_equals_local_bitwise(golden_dir, dtype):
+    """Placement invariance (ep.py:1-8): world-4 balanced plan, 4 sources, every
+    layer-2 rank share on its own weight slice, then one combine -- identical
+    bits to the all-local backend."""
+    banner(f"emulated ep4 {dtype}")
+    plan = json.loads((golden_dir / "plan_balanced.json").read_text())
+    p = Placement.from_plan(plan, device=DEV)
+    L = workloads.make_layer(8192 if dtype == torch.bfloat16 else 1024, seed=4, zipf_s=1.1)
+    x = L.x.to(dtype).to(DEV)
+    wi, wo = L.w_in.to(dtype).to(DEV), L.w_out.to(dtype).to(DEV)
+    idx, gate = route(x, L.w_router.to(dtype).to(DEV), 8)
+    n = x.shape[0]
+    local = HipMoEBackend(wi, wo)(x, idx, gate)
+    ep = EmulatedEPMoEBackend(2, p, 4, wi, wo)
+    got = ep(x, idx, gate, seg_tokens=[n * s // 4 for s in range(5)])
+    assert torch.equal(local, got)
+
+
+def test_rank_share_rows_match_oracle(golden_dir):
+    banner("rank share rows")
+    plan = json.loads((golden_dir / "plan_balanced.json").read_text())
+    p = Placement.from_plan(plan, device=DEV)
+    L = workloads.make_layer(8192, seed=5, zipf_s=1.1)
+    x = L.x.to(torch.bfloat16).to(DEV)
+    idx, _ = route(x, L.w_router.to(torch.bfloat16).to(DEV), 8)
+    r = 1
+    ids = p.experts_of_rank(r)[2]
+    be = HipEPShareBackend(2, p, r, L.w_in[ids].to(torch.bfloat16).to(DEV),
+                           L.w_out[ids].to(torch.bfloat16).to(DEV))
+    disp, y = be.share(x, idx, seg_tokens=[0, 2048, 4096, 6144, 8192])
+    M = int(disp.offsets[-1])
+    perm = to_np(disp.perm)[:M]
+    rows = perm[np.random.default_rng(0).choice(M, min(M, 2048), replace=False)]
+    xr = L.x.to(torch.bfloat16).float().numpy()
+    g2l = {e: i for i, e in enumerate(ids)}
+    eids = np.array([g2l[int(e)] for e in to_np(idx).reshape(-1)[rows]])
+    ref = O.experts(xr[rows // 8], eids, L.w_in[ids].to(torch.bfloat16).float().numpy(),
+                    L.w_out[ids].to(torch.bfloat16).float().numpy(), act_bf16=True, out_bf16=True)
+    assert rel_err(to_np(y)[rows], ref) <= TOL_BF16

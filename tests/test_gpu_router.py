@@ -1,0 +1,107 @@
+"""Router parity on the GPU (mep_router_topk, mep_topk_softmax) vs the oracle.
+
+Bar: indices bit-exact given the same fp32 logits (including tied logits,
+resolved lower-id-first on both sides); gates within 1 ulp-scale tolerance;
+fused-router logits within fp32 accumulation noise of the float64 oracle.
+"""
+import numpy as np
+import pytest
+import torch
+
+from helpers import banner, rel_err, to_np
+from miniep_amd import ops, workloads
+from oracle import moe_oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+@pytest.mark.parametrize("n,e,k", [(4096, 32, 8), (1001, 32, 8), (77, 16, 4), (300, 64, 8),
+                                   (129, 256, 8), (50, 8, 8), (33, 32, 1)])
+@pytest.mark.parametrize("gate_dtype", [torch.float32, torch.bfloat16])
+def test_topk_softmax_bit_exact(n, e, k, gate_dtype):
+    banner(f"topk_softmax n={n} e={e} k={k} gate={gate_dtype}")
+    g = torch.Generator().manual_seed(n * 7 + e)
+    lg = torch.randn(n, e, generator=g) * 2
+    idx, gate = ops.topk_softmax(lg.to(DEV), k, gate_dtype)
+    ridx, rgate = O.topk_softmax(lg.numpy(), k, gate_bf16=gate_dtype == torch.bfloat16)
+    assert np.array_equal(to_np(idx), ridx)
+    tol = 2 ** -8 if gate_dtype == torch.bfloat16 else 2e-6
+    assert np.abs(to_np(gate) - rgate).max() <= tol
+
+
+def test_topk_softmax_ties_lower_id_first():
+    banner("topk_softmax ties")
+    g = torch.Generator().manual_seed(5)
+    lg = torch.randint(-2, 3, (2000, 32), generator=g).float()
+    lg[0] = 0.0                                     # all equal
+    lg[1, :] = -0.0
+    lg[1, 7] = 0.0                                  # -0.0 == +0.0
+    idx, gate = ops.topk_softmax(lg.to(DEV), 8)
+    ridx, rgate = O.topk_softmax(lg.numpy(), 8)
+    assert np.array_equal(to_np(idx), ridx)
+    assert to_np(idx)[0].tolist() == list(range(8))
+    np.testing.assert_allclose(to_np(gate), rgate, rtol=2e-6)
+
+
+def test_topk_matches_torch_on_tie_free_rows():
+    banner("topk vs torch.topk")
+    g = torch.Generator().manual_seed(6)
+    lg = torch.randn(4096, 32, generator=g)
+    ref_v, ref_i = lg.topk(8, dim=-1)
+    idx, gate = ops.topk_softmax(lg.to(DEV), 8)
+    assert torch.equal(idx.cpu(), ref_i)
+    torch.testing.assert_close(gate.cpu(), torch.softmax(ref_v, -1), rtol=2e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("n,e", [(512, 32), (1000, 32), (16384, 32), (100, 16), (100, 64), (1, 32)])
+def test_router_fused(dtype, n, e):
+    banner(f"router n={n} e={e} dtype={dtype}")
+    g = torch.Generator().manual_seed(11 + n)
+    x = torch.randn(n, 1024, generator=g).to(dtype)
+    w = (torch.randn(e, 1024, generator=g) * 0.02).to(dtype)
+    k = 8
+    idx, gate, logits = ops.router_topk(x.to(DEV), w.to(DEV), k, return_logits=True)
+    xr, wr = x.float().numpy(), w.float().numpy()
+    ref_logits = O.router_logits(xr, wr)
+    lg = to_np(logits)
+    # fp32 accumulation of 1024 exact products vs the float64 sum
+    assert np.abs(lg - ref_logits).max() <= 1e-5 * np.abs(ref_logits).max() + 1e-6
+    # selection + softmax bit-exact given the kernel's own fp32 logits
+    ridx, rgate = O.topk_softmax(lg, k, gate_bf16=dtype == torch.bfloat16)
+    assert np.array_equal(to_np(idx), ridx)
+    tol = 2 ** -8 if dtype == torch.bfloat16 else 2e-6
+    assert np.abs(to_np(gate) - rgate).max() <= tol
+    # and equal to the oracle's own routing wherever its top-9 gaps exceed the logit noise
+    oidx, _ = O.topk_softmax(ref_logits, k)
+    s = -np.sort(-ref_logits, axis=1)
+    clear = (np.diff(-s[:, : k + 1], axis=1) > 1e-4).all(axis=1)
+    assert clear.mean() > 0.9
+    assert np.array_equal(to_np(idx)[clear], oidx[clear])
+
+
+def test_router_skewed_layer_routing_counts():
+    """Full-size skewed layer: per-expert counts from the kernel's routing equal
+    the oracle's selection on the kernel logits (bit-exact)."""
+    banner("router skewed t=16384")
+    L = workloads.make_layer(16384, seed=0, zipf_s=1.2)
+    x = L.x.to(torch.bfloat16).to(DEV)
+    w = L.w_router.to(torch.bfloat16).to(DEV)
+    idx, gate, logits = ops.router_topk(x, w, 8, return_logits=True)
+    ridx, _ = O.topk_softmax(to_np(logits), 8)
+    assert np.array_equal(to_np(idx), ridx)
+    counts = np.bincount(ridx.reshape(-1), minlength=32)
+    assert counts.max() / counts.mean() > 3.5
+
+
+def test_router_rejects_bad_shapes():
+    banner("router errors")
+    x = torch.randn(4, 1000, device=DEV)
+    w = torch.randn(32, 1000, device=DEV)
+    with pytest.raises(RuntimeError, match="multiple of 256"):
+        ops.router_topk(x, w, 8)
+    with pytest.raises(RuntimeError, match="n_experts"):
+        ops.router_topk(torch.randn(4, 256, device=DEV), torch.randn(48, 256, device=DEV), 8)
+    idx, gate = ops.router_topk(torch.randn(0, 256, device=DEV), torch.randn(32, 256, device=DEV), 8)
+    assert idx.shape == (0, 8)

@@ -1,0 +1,80 @@
+"""Host-side tests that need no GPU: the C-ABI library, plan I/O and the balancer.
+
+The balancer KAT is the one reference-held golden vector of the path:
+results/plan_balanced.json is the reference's plan_balanced() output for the
+summed routing counts of results/bench_naive.json at world 4 with 2 replica
+slots per rank (scripts/make_plan.py:24-29).
+"""
+import ctypes
+import json
+
+import numpy as np
+import pytest
+import torch
+
+from miniep_amd import Placement, _lib, plan_balanced
+from oracle import moe_oracle as O
+
+
+def test_library_exports_every_header_function():
+    L = _lib.lib()
+    names = _lib.header_functions()
+    assert len(names) == 12
+    for n in names:
+        assert hasattr(L, n), n
+    assert L.mep_abi_version() == 1
+    assert _lib.last_error() == ""
+
+
+def test_workspace_size_queries():
+    L = _lib.lib()
+    seg = (ctypes.c_int64 * 2)(0, 16384)
+    ws = L.mep_dispatch_workspace_size(16384, 8, 32, 1, seg)
+    # header + 2 flag words per block + rr snapshot + per-block histograms (128 blocks)
+    assert ws >= 256 + 8 * 128 + 8 * 32 + 4 * 128 * 32
+    seg4 = (ctypes.c_int64 * 5)(0, 2048, 4096, 6144, 8192)
+    assert L.mep_dispatch_workspace_size(8192, 8, 32, 4, seg4) >= 4 * 32 * 8
+    assert L.mep_dispatch_workspace_size(10, 8, 32, 17, None) >= 0
+    assert L.mep_experts_workspace_size(131072, 512, _lib.DTYPE_BF16) >= 131072 * 512 * 2
+    assert L.mep_experts_workspace_size(4096, 512, _lib.DTYPE_F32) >= 4096 * 512 * 4
+    assert L.mep_experts_workspace_size(4096, 512, 7) == 0
+
+
+def test_plan_balanced_reproduces_reference_plan(golden_dir):
+    rc = json.loads((golden_dir / "route_counts_bench_naive.json").read_text())
+    ref = json.loads((golden_dir / "plan_balanced.json").read_text())
+    placement, report = plan_balanced(torch.tensor(rc["counts"]), rc["world"],
+                                      slots_per_rank=rc["slots_per_rank"],
+                                      target_ratio=rc["target_ratio"], device="cpu")
+    assert placement.to_plan() == ref
+    # README.md of the reference: 71 replicas in the balanced plan
+    assert report["replicas_total"] == 71
+    assert all(l["imbalance_after"] <= l["imbalance_before"] for l in report["layers"])
+
+
+def test_placement_plan_io_and_tables(golden_dir):
+    plan = json.loads((golden_dir / "plan_balanced.json").read_text())
+    p = Placement.from_plan(plan, device="cpu")
+    assert p.to_plan() == plan
+    assert p.num_layers == 24 and p.num_experts == 32
+    # layer 2: 8 owned + 2 replica experts on every rank
+    for r in range(4):
+        assert len(p.experts_of_rank(r)[2]) == 10
+    for l in range(24):
+        t_ref, n_ref = O.build_table(p.owners[l])
+        t, n = p.tables(l)
+        assert np.array_equal(t.numpy(), t_ref) and np.array_equal(n.numpy(), n_ref)
+        assert p.has_replicas(l) == bool((n_ref != 1).any())
+    naive = Placement.naive(24, 32, 4, device="cpu")
+    assert naive.experts_of_rank(3)[0] == list(range(24, 32))
+    assert not naive.has_replicas(0)
+    with pytest.raises(ValueError):
+        Placement.naive(1, 30, 4, device="cpu")
+    with pytest.raises(ValueError):
+        Placement([[[0], []]], device="cpu")
+
+
+def test_ops_reject_cpu_tensors():
+    from miniep_amd import ops
+    with pytest.raises(RuntimeError, match="GPU only"):
+        ops.router_topk(torch.zeros(4, 256), torch.zeros(32, 256), 8)
