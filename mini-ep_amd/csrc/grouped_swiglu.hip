@@ -12,41 +12,47 @@
 //   GEMM-2  y_entries[perm[r], :] = act[r, :] W_out^T
 //           rows are scattered straight to their (token, slot) cell.
 //
-// Tiling: BM x BN output tile per workgroup, K staged 128 bytes per row at a
-// time (64 bf16 / 32 fp32) through double-buffered LDS with one barrier per
-// K step; the next K step's global loads are in flight while the current one
-// feeds the MFMAs.  LDS rows are 8 chunks of 16 B with the chunk index XOR-ed
-// by (row & 7), which makes both the 16-byte stores and the MFMA fragment
-// reads (16 rows x one chunk) bank-conflict free.
+// Tiling: BM x BN output tile, 8 waves (4 x 2) of 64 x 128.  K is staged 128
+// bytes per row at a time (64 bf16 / 32 fp32) through two LDS stages filled by
+// global_load_lds_dwordx4 (global memory straight into LDS, no VGPR staging):
+// one instruction moves 8 rows x 128 B; lane L lands at byte 16 L, so it
+// fetches logical chunk (L%8) ^ (L/8) of its row, which stores each row's
+// chunks XOR-swizzled by (row & 7) and makes the fragment reads (16 rows x one
+// chunk) bank-conflict free.  The MFMA takes the weight fragment as its first
+// operand, so it produces C^T: each lane holds 4 consecutive output columns of
+// one row, and the epilogue packs them into 8-byte LDS writes.
 // MFMA: v_mfma_f32_16x16x32_bf16 (bf16) or 4 x v_mfma_f32_16x16x4_f32 per
 // 16-byte chunk (fp32); accumulation is fp32 in both cases.
 //
-// Scheduling: the ragged tile list (expert, m-tile, n-tile) is derived on the
-// device from `offsets`, so no host round trip is needed for the counts.  The
-// grid is an upper bound; workgroup b runs logical tile
-//   (b mod 8) * ceil(T/8) + b / 8
-// so the 32 CUs of one XCD (workgroups are dealt to the 8 XCDs round-robin)
-// sweep one contiguous run of tiles and share its weights and rows in their L2.
+// Scheduling: persistent.  One workgroup per CU walks a list of tiles
+// (expert, m-tile, n-tile) derived on the device from `offsets` (no host round
+// trip for the counts).  Workgroups are dealt to the 8 XCDs round-robin, so
+// workgroup b takes tiles (b mod 8) * ceil(T/8) + b/8 + i * (grid/8): the CUs
+// of one XCD sweep one contiguous run of tiles and share weights and rows in
+// their L2.  While a tile's epilogue drains through one LDS stage, the next
+// tile's first K step is already streaming into the other.
 #include "common.h"
 
 namespace mep {
 namespace {
 
 constexpr int kRowBytes = 128;   // K bytes per row per LDS stage
-constexpr int kChunks = 8;       // 16-byte chunks per LDS row
+// s_waitcnt immediate for "vmcnt(0)" alone (gfx9 encoding: expcnt and lgkmcnt at max)
+constexpr int kVmcnt0 = 0x0F70;
 
 template <int BM_, int BN_, int WM_, int WN_>
 struct TileCfg {
   static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_;
   static constexpr int NT = WM * WN * 64;
+  static constexpr int NWAVES = WM * WN;
   static constexpr int BMW = BM / WM, BNW = BN / WN;
   static constexpr int MF = BMW / 16, NF = BNW / 16;
-  static constexpr int APT = BM * kChunks / NT;   // A chunks loaded per thread per stage
-  static constexpr int BPT = BN * kChunks / NT;   // B chunks loaded per thread per stage
   static constexpr int STAGE_BYTES = (BM + BN) * kRowBytes;
+  static constexpr int NBLK = (BM + BN) / 8;      // 1 KiB DMA blocks per stage
+  static constexpr int BPW = NBLK / NWAVES;       // blocks per wave per stage
   static_assert(BM % (16 * WM) == 0 && BN % (16 * WN) == 0, "tile / wave shape");
   static_assert(NF % 2 == 0, "gate and up halves need an even number of 16-col fragments");
-  static_assert((BM * kChunks) % NT == 0 && (BN * kChunks) % NT == 0, "load split");
+  static_assert(NBLK % NWAVES == 0 && (BM / 8) % BPW == 0, "a wave's blocks are all A or all B rows");
 };
 
 struct GemmParams {
@@ -62,7 +68,13 @@ struct GemmParams {
   int n_tiles_n;             // column tiles per row tile
 };
 
-__device__ __forceinline__ float silu_f(float v) { return v / (1.0f + expf(-v)); }
+// silu(v) = v / (1 + e^-v) with the hardware exp2 and reciprocal (about 1 ulp
+// each); saturates correctly: v -> -inf gives -0, v -> +inf gives v.
+__device__ __forceinline__ float silu_f(float v) {
+  return v * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-v * 1.4426950408889634f));
+}
+
+constexpr int pow2_floor(int v) { int r = 1; while (r * 2 <= v) r *= 2; return r; }
 
 template <int DT, class Cfg, bool GEMM1>
 __global__ __launch_bounds__(Cfg::NT) void grouped_gemm_kernel(GemmParams p) {
@@ -71,211 +83,266 @@ __global__ __launch_bounds__(Cfg::NT) void grouped_gemm_kernel(GemmParams p) {
   constexpr int EPC = 16 / EB;                     // elements per 16-byte chunk
   constexpr int BKE = kRowBytes / EB;              // K elements per stage
   constexpr int BM = Cfg::BM, BN = Cfg::BN, NT = Cfg::NT;
-  constexpr int MF = Cfg::MF, NF = Cfg::NF;
+  constexpr int MF = Cfg::MF, NF = Cfg::NF, BPW = Cfg::BPW;
+  constexpr int STAGE = Cfg::STAGE_BYTES;
   constexpr int CN = GEMM1 ? BN / 2 : BN;          // output columns per tile
-  constexpr int C_LD = CN * EB + 16;               // staging row stride (bytes)
-  constexpr int SMEM = (2 * Cfg::STAGE_BYTES > BM * C_LD) ? 2 * Cfg::STAGE_BYTES : BM * C_LD;
-  __shared__ __attribute__((aligned(16))) unsigned char smem[SMEM];
-  __shared__ int s_prefix[257];
-  __shared__ int s_tile[4];
+  // epilogue staging through one stage: PASS_COLS columns of all BM rows at a time
+  constexpr int PASS_COLS = pow2_floor(STAGE / (BM * EB)) < CN ? pow2_floor(STAGE / (BM * EB)) : CN;
+  constexpr int NPASS = CN / PASS_COLS;
+  constexpr int SROW = PASS_COLS * EB;             // staging row bytes
+  constexpr int SCPR = SROW / 16;                  // 16-byte chunks per staging row
+  static_assert(CN % PASS_COLS == 0 && SCPR >= 1 && (SCPR & (SCPR - 1)) == 0, "staging geometry");
+  static_assert(PASS_COLS % 16 == 0, "a 16-column fragment never straddles two passes");
+
+  // One LDS object only: with a second __shared__ variable the compiler tags
+  // LDS accesses with alias scopes and then makes every fragment read wait for
+  // the in-flight DMA into the other stage (vmcnt(0)), which serialises the
+  // pipeline.  The schedule tables therefore live at the end of `smem`.
+  constexpr int NLMAX = 256;
+  __shared__ __attribute__((aligned(16))) unsigned char smem[2 * STAGE + (2 * NLMAX + 2) * 4];
+  int* const s_prefix = reinterpret_cast<int*>(smem + 2 * STAGE);   // [NLMAX + 1] tiles before expert j
+  int* const s_off = s_prefix + NLMAX + 1;                          // [NLMAX + 1] row offsets
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
-
-  // ---- tile schedule from the device-side offsets --------------------------
+  const int K = p.K;
   const int nl = p.n_local;
-  for (int j = tid; j < nl; j += NT) {
-    const int rows = p.offsets[j + 1] - p.offsets[j];
-    s_prefix[j + 1] = ((rows + BM - 1) / BM) * p.n_tiles_n;
-  }
+
+  // ---- tile table: tiles per expert, prefix over experts ---------------------
+  for (int j = tid; j <= nl; j += NT) s_off[j] = p.offsets[j];
+  __syncthreads();
+  for (int j = tid; j < nl; j += NT)
+    s_prefix[j + 1] = ((s_off[j + 1] - s_off[j] + BM - 1) / BM) * p.n_tiles_n;
   if (tid == 0) s_prefix[0] = 0;
   __syncthreads();
-  if (tid == 0) {
+  if (tid == 0)
     for (int j = 0; j < nl; ++j) s_prefix[j + 1] += s_prefix[j];
-  }
   __syncthreads();
   const int total = s_prefix[nl];
   const int per_xcd = (total + 7) / 8;
-  const int slot = blockIdx.x / 8;
-  if (slot >= per_xcd) return;
-  const int lt = (blockIdx.x % 8) * per_xcd + slot;
-  if (lt >= total) return;
-  if (tid == 0) s_tile[0] = -1;
-  __syncthreads();
-  for (int j = tid; j < nl; j += NT) {
-    if (lt >= s_prefix[j] && lt < s_prefix[j + 1]) {
-      const int u = lt - s_prefix[j];
-      s_tile[0] = j;
-      s_tile[1] = p.offsets[j] + (u / p.n_tiles_n) * BM;
-      s_tile[2] = p.offsets[j + 1];
-      s_tile[3] = u % p.n_tiles_n;
-    }
-  }
-  __syncthreads();
-  const int e = s_tile[0];
-  if (e < 0) return;
-  const int row0 = s_tile[1], row_end = s_tile[2], nt = s_tile[3];
-  const int K = p.K;
+  const int xcd = blockIdx.x % 8, slot = blockIdx.x / 8, nslots = gridDim.x / 8;
+  const int n_my = slot < per_xcd ? (per_xcd - slot + nslots - 1) / nslots : 0;
+  // tiles of this workgroup: xcd * per_xcd + slot + i * nslots, i < n_my, below total
+  auto tile_id = [&](int i) { return xcd * per_xcd + slot + i * nslots; };
+  auto tile_valid = [&](int i) { return i < n_my && tile_id(i) < total; };
+  if (!tile_valid(0)) return;
 
-  // ---- global source pointers of the chunks this thread stages -------------
-  const T* a_src[Cfg::APT];
-  const T* b_src[Cfg::BPT];
-  const int ch = tid % kChunks;
-#pragma unroll
-  for (int i = 0; i < Cfg::APT; ++i) {
-    const int r = tid / kChunks + i * (NT / kChunks);
-    const int row = (row0 + r < row_end) ? row0 + r : row0;   // tail rows: any valid row
-    int64_t src;
-    if constexpr (GEMM1) src = p.perm[row] / p.top_k;
-    else src = row;
-    a_src[i] = static_cast<const T*>(p.A) + src * K + ch * EPC;
-  }
-  const T* wexp = static_cast<const T*>(p.W) + static_cast<int64_t>(e) * p.w_expert_stride;
-#pragma unroll
-  for (int i = 0; i < Cfg::BPT; ++i) {
-    const int r = tid / kChunks + i * (NT / kChunks);
-    int wrow;
-    if constexpr (GEMM1) wrow = (r < BN / 2) ? nt * (BN / 2) + r : p.N + nt * (BN / 2) + (r - BN / 2);
-    else wrow = nt * BN + r;
-    b_src[i] = wexp + static_cast<int64_t>(wrow) * K + ch * EPC;
-  }
-
-  u32x4 ra[Cfg::APT], rb[Cfg::BPT];
-  auto load_global = [&](int kt) {
-    const int koff = kt * BKE;
-#pragma unroll
-    for (int i = 0; i < Cfg::APT; ++i) ra[i] = *reinterpret_cast<const u32x4*>(a_src[i] + koff);
-#pragma unroll
-    for (int i = 0; i < Cfg::BPT; ++i) rb[i] = *reinterpret_cast<const u32x4*>(b_src[i] + koff);
-  };
-  auto store_lds = [&](int st) {
-    unsigned char* As = smem + st * Cfg::STAGE_BYTES;
-    unsigned char* Bs = As + BM * kRowBytes;
-#pragma unroll
-    for (int i = 0; i < Cfg::APT; ++i) {
-      const int r = tid / kChunks + i * (NT / kChunks);
-      *reinterpret_cast<u32x4*>(As + r * kRowBytes + ((ch ^ (r & 7)) << 4)) = ra[i];
+  struct Tile { int e, row0, row_end, nt; };
+  auto decode = [&](int lt) {
+    int lo = 0, hi = nl - 1;                       // largest j with s_prefix[j] <= lt
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (s_prefix[mid] <= lt) lo = mid; else hi = mid - 1;
     }
-#pragma unroll
-    for (int i = 0; i < Cfg::BPT; ++i) {
-      const int r = tid / kChunks + i * (NT / kChunks);
-      *reinterpret_cast<u32x4*>(Bs + r * kRowBytes + ((ch ^ (r & 7)) << 4)) = rb[i];
-    }
+    const int u = lt - s_prefix[lo];
+    Tile t;
+    t.e = lo;
+    t.row0 = s_off[lo] + (u / p.n_tiles_n) * BM;
+    t.row_end = s_off[lo + 1];
+    t.nt = u % p.n_tiles_n;
+    return t;
   };
 
-  f32x4 acc[MF][NF];
+  // ---- direct global -> LDS staging -------------------------------------------
+  // Wave w moves stage blocks w*BPW .. w*BPW+BPW-1 (block q = stage rows 8q..8q+7;
+  // A rows [0, BM), B rows [BM, BM + BN)).  Each lane keeps one 32-bit byte
+  // offset per block from a wave-uniform base (x / act, or the expert's W).
+  const int lrow = lane >> 3, lchunk = (lane & 7) ^ lrow;
+  const bool wave_loads_a = (wave * BPW) * 8 < BM;
+  uint32_t src_off[BPW];
+  const unsigned char* g_base;
+  auto setup = [&](const Tile& t) {
+    // recompute the per-lane row terms here instead of keeping them live across
+    // the whole tile loop (hoisted, they outgrow the register budget and spill)
+    int lrow_v = lrow, lchunk_v = lchunk;
+    asm volatile("" : "+v"(lrow_v), "+v"(lchunk_v));
+    if (wave_loads_a) {
+      g_base = static_cast<const unsigned char*>(p.A);
 #pragma unroll
-  for (int i = 0; i < MF; ++i)
+      for (int i = 0; i < BPW; ++i) {
+        const int r = (wave * BPW + i) * 8 + lrow_v;
+        const int row = (t.row0 + r < t.row_end) ? t.row0 + r : t.row0;   // tail rows: any valid row
+        int64_t src_row;
+        if constexpr (GEMM1) src_row = p.perm[row] / p.top_k;
+        else src_row = row;
+        src_off[i] = static_cast<uint32_t>((src_row * K + lchunk_v * EPC) * EB);
+      }
+    } else {
+      g_base = static_cast<const unsigned char*>(p.W) + static_cast<int64_t>(t.e) * p.w_expert_stride * EB;
 #pragma unroll
-    for (int j = 0; j < NF; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int i = 0; i < BPW; ++i) {
+        const int rb = (wave * BPW + i) * 8 + lrow_v - BM;
+        int wrow;
+        if constexpr (GEMM1) wrow = (rb < BN / 2) ? t.nt * (BN / 2) + rb : p.N + t.nt * (BN / 2) + (rb - BN / 2);
+        else wrow = t.nt * BN + rb;
+        src_off[i] = static_cast<uint32_t>((static_cast<int64_t>(wrow) * K + lchunk_v * EPC) * EB);
+      }
+    }
+  };
+  auto load_stage = [&](int kt, unsigned char* stage) {
+    const uint32_t koff = static_cast<uint32_t>(kt * kRowBytes);
+#pragma unroll
+    for (int i = 0; i < BPW; ++i)
+      __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)(g_base + src_off[i] + koff),
+                                       (__attribute__((address_space(3))) void*)(stage + (wave * BPW + i) * 1024),
+                                       16, 0, 0);
+  };
 
-  // fragment rows (within the LDS tile) this lane reads
+  // ---- fragments and MFMAs ------------------------------------------------------
+  // Lane (lr, lg) reads 16 B of row base + 16 i + lr at physical chunk
+  // (4 kk + lg) ^ (lr & 7): one per-lane base per fragment set plus immediates.
   const int lr = lane & 15, lg = lane >> 4;
-  int a_row[MF], b_row[NF];
+  uint32_t cp[2];
 #pragma unroll
-  for (int i = 0; i < MF; ++i) a_row[i] = wm * Cfg::BMW + i * 16 + lr;
-#pragma unroll
-  for (int j = 0; j < NF; ++j) {
-    if constexpr (GEMM1)
-      b_row[j] = (j < NF / 2) ? wn * (Cfg::BNW / 2) + j * 16 + lr
-                              : BN / 2 + wn * (Cfg::BNW / 2) + (j - NF / 2) * 16 + lr;
-    else
-      b_row[j] = wn * Cfg::BNW + j * 16 + lr;
+  for (int kk = 0; kk < 2; ++kk) cp[kk] = static_cast<uint32_t>(((kk * 4 + lg) ^ (lr & 7)) << 4);
+  const uint32_t a_lane = static_cast<uint32_t>((wm * Cfg::BMW + lr) * kRowBytes);
+  uint32_t b_lane_lo, b_lane_hi;   // GEMM-1: gate / up halves; GEMM-2: one contiguous range
+  if constexpr (GEMM1) {
+    b_lane_lo = static_cast<uint32_t>((BM + wn * (Cfg::BNW / 2) + lr) * kRowBytes);
+    b_lane_hi = static_cast<uint32_t>((BM + BN / 2 + wn * (Cfg::BNW / 2) + lr) * kRowBytes);
+  } else {
+    b_lane_lo = static_cast<uint32_t>((BM + wn * Cfg::BNW + lr) * kRowBytes);
+    b_lane_hi = b_lane_lo + (NF / 2) * 16 * kRowBytes;
   }
-
-  auto compute = [&](int st) {
-    const unsigned char* As = smem + st * Cfg::STAGE_BYTES;
-    const unsigned char* Bs = As + BM * kRowBytes;
+  f32x4 acc[MF][NF];
+  auto compute = [&](const unsigned char* S) {
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
-      const int c = kk * 4 + lg;
       u32x4 af[MF], bfr[NF];
 #pragma unroll
       for (int i = 0; i < MF; ++i)
-        af[i] = *reinterpret_cast<const u32x4*>(As + a_row[i] * kRowBytes + ((c ^ (a_row[i] & 7)) << 4));
+        af[i] = *reinterpret_cast<const u32x4*>(S + a_lane + cp[kk] + i * 16 * kRowBytes);
 #pragma unroll
-      for (int j = 0; j < NF; ++j)
-        bfr[j] = *reinterpret_cast<const u32x4*>(Bs + b_row[j] * kRowBytes + ((c ^ (b_row[j] & 7)) << 4));
+      for (int j = 0; j < NF; ++j) {
+        const uint32_t b = (j < NF / 2 ? b_lane_lo + j * 16 * kRowBytes : b_lane_hi + (j - NF / 2) * 16 * kRowBytes);
+        bfr[j] = *reinterpret_cast<const u32x4*>(S + b + cp[kk]);
+      }
+      // weight fragment first: the MFMA yields C^T (lane: one row, 4 columns)
 #pragma unroll
       for (int i = 0; i < MF; ++i)
 #pragma unroll
         for (int j = 0; j < NF; ++j) {
           if constexpr (DT == MEP_DTYPE_BF16) {
             acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                __builtin_bit_cast(bf16x8, af[i]), __builtin_bit_cast(bf16x8, bfr[j]), acc[i][j], 0, 0, 0);
+                __builtin_bit_cast(bf16x8, bfr[j]), __builtin_bit_cast(bf16x8, af[i]), acc[i][j], 0, 0, 0);
           } else {
             const float* a4 = reinterpret_cast<const float*>(&af[i]);
             const float* b4 = reinterpret_cast<const float*>(&bfr[j]);
 #pragma unroll
             for (int q = 0; q < 4; ++q)
-              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a4[q], b4[q], acc[i][j], 0, 0, 0);
+              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(b4[q], a4[q], acc[i][j], 0, 0, 0);
           }
         }
     }
   };
 
-  // ---- main loop -------------------------------------------------------------
-  const int KT = K / BKE;
-  load_global(0);
-  store_lds(0);
-  __syncthreads();
-  for (int kt = 0; kt < KT - 1; ++kt) {
-    load_global(kt + 1);
-    compute(kt & 1);
-    store_lds((kt + 1) & 1);
-    __syncthreads();
-  }
-  compute((KT - 1) & 1);
-  __syncthreads();
-
-  // ---- epilogue: registers -> LDS tile -> 16-byte row stores -----------------
-  // 16x16 MFMA C layout: lane holds rows 4*(lane/16) + i, column lane % 16.
+  // ---- epilogue helpers -----------------------------------------------------------
+  // Lane holds, for fragment (i, j), row wm*BMW + 16 i + lr and the 4 columns
+  // 16 j + 4 lg + q of its wave's column range.  Staging row r of a pass is
+  // SROW bytes with 16-byte chunks XOR-swizzled by (r & (SCPR-1)).
+  T* const C = static_cast<T*>(p.C);
+  auto stage_addr = [&](int r, int cbyte) {
+    return r * SROW + ((((cbyte >> 4) ^ (r & (SCPR - 1)))) << 4) + (cbyte & 15);
+  };
+  auto epilogue = [&](const Tile& t, unsigned char* S) {
 #pragma unroll
-  for (int i = 0; i < MF; ++i)
+    for (int pass = 0; pass < NPASS; ++pass) {
+      const int c0 = pass * PASS_COLS;
 #pragma unroll
-    for (int j = 0; j < (GEMM1 ? NF / 2 : NF); ++j)
+      for (int i = 0; i < MF; ++i) {
+        const int r = wm * Cfg::BMW + i * 16 + lr;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int r = wm * Cfg::BMW + i * 16 + lg * 4 + q;
-        int c;
-        float v;
-        if constexpr (GEMM1) {
-          c = wn * (Cfg::BNW / 2) + j * 16 + lr;
-          v = silu_f(acc[i][j][q]) * acc[i][j + NF / 2][q];
-        } else {
-          c = wn * Cfg::BNW + j * 16 + lr;
-          v = acc[i][j][q];
+        for (int j = 0; j < (GEMM1 ? NF / 2 : NF); ++j) {
+          const int c = (GEMM1 ? wn * (Cfg::BNW / 2) : wn * Cfg::BNW) + j * 16 + lg * 4;
+          if (c < c0 || c >= c0 + PASS_COLS) continue;             // wave-uniform
+          float v[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            v[q] = GEMM1 ? silu_f(acc[i][j][q]) * acc[i][j + NF / 2][q] : acc[i][j][q];
+          unsigned char* dst = S + stage_addr(r, (c - c0) * EB);
+          if constexpr (DT == MEP_DTYPE_BF16) {
+            uint2 w;
+            w.x = pack_bf16x2(v[0], v[1]);
+            w.y = pack_bf16x2(v[2], v[3]);
+            *reinterpret_cast<uint2*>(dst) = w;
+          } else {
+            *reinterpret_cast<f32x4*>(dst) = f32x4{v[0], v[1], v[2], v[3]};
+          }
         }
-        *reinterpret_cast<T*>(smem + r * C_LD + c * EB) = Elem<DT>::from_f32(v);
       }
-  __syncthreads();
-  constexpr int CPR = CN * EB / 16;   // 16-byte chunks per output row
-  T* C = static_cast<T*>(p.C);
-  for (int q = tid; q < BM * CPR; q += NT) {
-    const int r = q / CPR, c = q - r * CPR;
-    if (row0 + r >= row_end) continue;
-    int64_t dst;
-    if constexpr (GEMM1) dst = static_cast<int64_t>(row0 + r) * p.N + nt * CN + c * EPC;
-    else dst = static_cast<int64_t>(p.perm[row0 + r]) * p.N + nt * CN + c * EPC;
-    *reinterpret_cast<u32x4*>(C + dst) = *reinterpret_cast<const u32x4*>(smem + r * C_LD + c * 16);
+      __syncthreads();
+      for (int q = tid; q < BM * SCPR; q += NT) {
+        const int r = q / SCPR, ch = q % SCPR;
+        if (t.row0 + r >= t.row_end) continue;
+        int64_t dst;
+        if constexpr (GEMM1) dst = static_cast<int64_t>(t.row0 + r) * p.N;
+        else dst = static_cast<int64_t>(p.perm[t.row0 + r]) * p.N;
+        dst += t.nt * CN + c0 + ch * EPC;
+        *reinterpret_cast<u32x4*>(C + dst) = *reinterpret_cast<const u32x4*>(S + stage_addr(r, ch * 16));
+      }
+      __syncthreads();
+    }
+  };
+
+  // ---- persistent tile loop -------------------------------------------------------
+  // Per tile: step kt computes from stage kt&1 while step kt+1 streams into the
+  // other stage; each wave's vmcnt(0) plus the barrier publish it.  KT is even,
+  // so the last step reads stage 1 and stage 0 is free for the next tile's
+  // first step, which streams in while this tile's epilogue drains via stage 1.
+  unsigned char* const stage0 = smem;
+  unsigned char* const stage1 = smem + STAGE;
+  const int KT = K / BKE;
+  Tile cur = decode(tile_id(0));
+  setup(cur);
+  load_stage(0, stage0);
+  for (int it = 0; tile_valid(it); ++it) {
+#pragma unroll
+    for (int i = 0; i < MF; ++i)
+#pragma unroll
+      for (int j = 0; j < NF; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    __builtin_amdgcn_s_waitcnt(kVmcnt0);
+    __syncthreads();
+    for (int kt = 0; kt < KT - 1; ++kt) {
+      load_stage(kt + 1, (kt & 1) ? stage0 : stage1);
+      compute((kt & 1) ? stage1 : stage0);
+      __builtin_amdgcn_s_waitcnt(kVmcnt0);
+      __syncthreads();
+    }
+    compute(stage1);
+    __syncthreads();                               // every wave is done with both stages
+    const Tile done = cur;
+    if (tile_valid(it + 1)) {
+      cur = decode(tile_id(it + 1));
+      setup(cur);
+      load_stage(0, stage0);
+    }
+    epilogue(done, stage1);
   }
 }
 
 template <int DT, class Cfg, bool GEMM1>
 hipError_t launch(const GemmParams& p, int64_t max_rows, hipStream_t stream) {
+  static int n_cu = 0;
+  if (n_cu == 0) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n_cu <= 0)
+      n_cu = 256;
+  }
   int64_t tiles = ((max_rows + Cfg::BM - 1) / Cfg::BM + p.n_local) * p.n_tiles_n;
-  tiles = (tiles + 7) / 8 * 8;
   if (tiles == 0) return hipSuccess;
-  grouped_gemm_kernel<DT, Cfg, GEMM1><<<dim3(static_cast<unsigned>(tiles)), Cfg::NT, 0, stream>>>(p);
+  int64_t grid = tiles < n_cu ? tiles : n_cu;      // one persistent workgroup per CU
+  grid = (grid + 7) / 8 * 8;
+  grouped_gemm_kernel<DT, Cfg, GEMM1><<<dim3(static_cast<unsigned>(grid)), Cfg::NT, 0, stream>>>(p);
   return hipGetLastError();
 }
 
 // Tile shapes: bf16 256x256 (GEMM-1: 128 gate + 128 up columns) on 8 waves
-// (4 x 2, 64 x 128 per wave, 2 waves per SIMD, no spills);
-// fp32 64x128 on 4 waves.
+// (4 x 2, 64 x 128 per wave, 2 waves per SIMD, no spills); fp32 128x128 on
+// 4 waves.
 typedef TileCfg<256, 256, 4, 2> CfgBf16;
-typedef TileCfg<64, 128, 2, 2> CfgF32;
+typedef TileCfg<128, 128, 2, 2> CfgF32;
 
 template <int DT, class Cfg>
 int run_gate_up(const void* x, int top_k, const int32_t* perm, const int32_t* offsets, int n_local,
@@ -318,6 +385,10 @@ int check_expert_args(const char* fn, int64_t n_tokens, int top_k, int n_local, 
               "%s: inter %d must be a positive multiple of 128", fn, inter);
   MEP_REQUIRE(max_rows <= n_tokens * top_k, MEP_ERR_INVALID_ARG,
               "%s: max_rows %lld exceeds n_tokens * top_k", fn, (long long)max_rows);
+  // the kernels address x, act and one expert's weights with 32-bit byte offsets
+  const int64_t eb = dtype_bytes(dtype);
+  MEP_REQUIRE(n_tokens * hidden * eb < (int64_t(1) << 32) && max_rows * inter * eb < (int64_t(1) << 32),
+              MEP_ERR_UNSUPPORTED, "%s: x or act larger than 4 GiB", fn);
   return MEP_OK;
 }
 
