@@ -99,9 +99,10 @@ __global__ __launch_bounds__(Cfg::NT) void grouped_gemm_kernel(GemmParams p) {
   // the in-flight DMA into the other stage (vmcnt(0)), which serialises the
   // pipeline.  The schedule tables therefore live at the end of `smem`.
   constexpr int NLMAX = 256;
-  __shared__ __attribute__((aligned(16))) unsigned char smem[2 * STAGE + (2 * NLMAX + 2) * 4];
+  __shared__ __attribute__((aligned(16))) unsigned char smem[2 * STAGE + (2 * NLMAX + 2 + 2 * BM) * 4];
   int* const s_prefix = reinterpret_cast<int*>(smem + 2 * STAGE);   // [NLMAX + 1] tiles before expert j
   int* const s_off = s_prefix + NLMAX + 1;                          // [NLMAX + 1] row offsets
+  int* const s_rows = s_off + NLMAX + 1;                            // [2][BM] perm of the tile rows
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -152,7 +153,12 @@ __global__ __launch_bounds__(Cfg::NT) void grouped_gemm_kernel(GemmParams p) {
   const bool wave_loads_a = (wave * BPW) * 8 < BM;
   uint32_t src_off[BPW];
   const unsigned char* g_base;
-  auto setup = [&](const Tile& t) {
+  auto setup = [&](const Tile& t, int parity) {
+    if constexpr (!GEMM1) {
+      // destinations of this tile's rows for the scatter epilogue
+      for (int r = tid; r < BM; r += NT)
+        s_rows[parity * BM + r] = (t.row0 + r < t.row_end) ? p.perm[t.row0 + r] : 0;
+    }
     // recompute the per-lane row terms here instead of keeping them live across
     // the whole tile loop (hoisted, they outgrow the register budget and spill)
     int lrow_v = lrow, lchunk_v = lchunk;
@@ -245,7 +251,7 @@ __global__ __launch_bounds__(Cfg::NT) void grouped_gemm_kernel(GemmParams p) {
   auto stage_addr = [&](int r, int cbyte) {
     return r * SROW + ((((cbyte >> 4) ^ (r & (SCPR - 1)))) << 4) + (cbyte & 15);
   };
-  auto epilogue = [&](const Tile& t, unsigned char* S) {
+  auto epilogue = [&](const Tile& t, int parity, unsigned char* S) {
 #pragma unroll
     for (int pass = 0; pass < NPASS; ++pass) {
       const int c0 = pass * PASS_COLS;
@@ -277,7 +283,7 @@ __global__ __launch_bounds__(Cfg::NT) void grouped_gemm_kernel(GemmParams p) {
         if (t.row0 + r >= t.row_end) continue;
         int64_t dst;
         if constexpr (GEMM1) dst = static_cast<int64_t>(t.row0 + r) * p.N;
-        else dst = static_cast<int64_t>(p.perm[t.row0 + r]) * p.N;
+        else dst = static_cast<int64_t>(s_rows[parity * BM + r]) * p.N;
         dst += t.nt * CN + c0 + ch * EPC;
         *reinterpret_cast<u32x4*>(C + dst) = *reinterpret_cast<const u32x4*>(S + stage_addr(r, ch * 16));
       }
@@ -294,7 +300,7 @@ __global__ __launch_bounds__(Cfg::NT) void grouped_gemm_kernel(GemmParams p) {
   unsigned char* const stage1 = smem + STAGE;
   const int KT = K / BKE;
   Tile cur = decode(tile_id(0));
-  setup(cur);
+  setup(cur, 0);
   load_stage(0, stage0);
   for (int it = 0; tile_valid(it); ++it) {
 #pragma unroll
@@ -314,10 +320,10 @@ __global__ __launch_bounds__(Cfg::NT) void grouped_gemm_kernel(GemmParams p) {
     const Tile done = cur;
     if (tile_valid(it + 1)) {
       cur = decode(tile_id(it + 1));
-      setup(cur);
+      setup(cur, (it + 1) & 1);
       load_stage(0, stage0);
     }
-    epilogue(done, stage1);
+    epilogue(done, it & 1, stage1);
   }
 }
 
