@@ -1,0 +1,81 @@
+"""The raw C ABI through ctypes, exactly as a binding would call it (no
+miniep_amd wrapper): must give the same bits as the HipMoEBackend path."""
+import ctypes
+
+import pytest
+import torch
+
+from helpers import banner
+from miniep_amd import HipMoEBackend, _lib, route, workloads
+
+pytestmark = pytest.mark.gpu
+
+
+def _moe_layer_raw(L, x, w_r, w_in, w_out, k=8):
+    vp, i64 = ctypes.c_void_p, ctypes.c_int64
+    N, H = x.shape
+    E = w_r.shape[0]
+    I = w_out.shape[2]
+    BF16 = 1
+    s = torch.cuda.current_stream().cuda_stream
+
+    def ok(rc):
+        if rc != 0:
+            raise RuntimeError(L.mep_last_error().decode())
+
+    idx = torch.empty(N, k, dtype=torch.int64, device="cuda")
+    gate = torch.empty(N, k, dtype=x.dtype, device="cuda")
+    ok(L.mep_router_topk(x.data_ptr(), w_r.data_ptr(), N, H, E, k, BF16, idx.data_ptr(), gate.data_ptr(),
+                         None, s))
+    seg = (i64 * 2)(0, N)
+    ws = torch.empty(L.mep_dispatch_workspace_size(N, k, E, 1, seg), dtype=torch.uint8, device="cuda")
+    table = torch.zeros(E, 1, dtype=torch.int32, device="cuda")
+    n_rep = torch.ones(E, dtype=torch.int32, device="cuda")
+    g2l = torch.arange(E, dtype=torch.int32, device="cuda")
+    counts = torch.empty(E, dtype=torch.int32, device="cuda")
+    offsets = torch.empty(E + 1, dtype=torch.int32, device="cuda")
+    perm = torch.empty(N * k, dtype=torch.int32, device="cuda")
+    row = torch.empty(N * k, dtype=torch.int32, device="cuda")
+    ok(L.mep_dispatch(idx.data_ptr(), None, N, k, E, table.data_ptr(), n_rep.data_ptr(), 1, 0, None, seg, 1, 0,
+                      g2l.data_ptr(), E, counts.data_ptr(), offsets.data_ptr(), perm.data_ptr(), row.data_ptr(),
+                      None, None, ws.data_ptr(), ws.numel(), s))
+    ok(L.mep_dispatch_check(ws.data_ptr(), s))
+    act = torch.empty(L.mep_experts_workspace_size(N * k, I, BF16), dtype=torch.uint8, device="cuda")
+    y = torch.empty(N * k, H, dtype=x.dtype, device="cuda")
+    ok(L.mep_grouped_swiglu(x.data_ptr(), N, k, perm.data_ptr(), offsets.data_ptr(), E, N * k, w_in.data_ptr(),
+                            w_out.data_ptr(), H, I, BF16, y.data_ptr(), act.data_ptr(), act.numel(), s))
+    out = torch.empty(N, H, dtype=x.dtype, device="cuda")
+    ok(L.mep_combine(y.data_ptr(), gate.data_ptr(), row.data_ptr(), None, N, k, H, BF16, out.data_ptr(), s))
+    return out, idx, gate
+
+
+def test_raw_ctypes_layer_matches_backend():
+    banner("raw C ABI layer")
+    L = _lib.lib()          # signatures are registered by the loader
+    layer = workloads.make_layer(2048, seed=9, zipf_s=1.2)
+    bf = torch.bfloat16
+    x = layer.x.to(bf).cuda()
+    w_r = layer.w_router.to(bf).cuda()
+    w_in = layer.w_in.to(bf).cuda()
+    w_out = layer.w_out.to(bf).cuda()
+    out, idx, gate = _moe_layer_raw(L, x, w_r, w_in, w_out)
+    idx2, gate2 = route(x, w_r, 8)
+    ref = HipMoEBackend(w_in, w_out)(x, idx2, gate2)
+    assert torch.equal(idx, idx2) and torch.equal(gate, gate2)
+    assert torch.equal(out, ref)
+
+
+def test_error_codes_and_messages():
+    banner("C ABI errors")
+    L = _lib.lib()
+    x = torch.zeros(4, 1000, dtype=torch.bfloat16, device="cuda")
+    rc = L.mep_router_topk(x.data_ptr(), x.data_ptr(), 4, 1000, 32, 8, 1, x.data_ptr(), x.data_ptr(), None, None)
+    assert rc == _lib.ERR_UNSUPPORTED and b"multiple of 256" in L.mep_last_error()
+    rc = L.mep_router_topk(x.data_ptr(), x.data_ptr(), 4, 1024, 32, 8, 7, x.data_ptr(), x.data_ptr(), None, None)
+    assert rc == _lib.ERR_INVALID_ARG
+    rc = L.mep_combine(None, None, None, None, 4, 8, 1024, 1, None, None)
+    assert rc == _lib.ERR_INVALID_ARG
+    rc = L.mep_grouped_swiglu(x.data_ptr(), 4, 8, x.data_ptr(), x.data_ptr(), 4, 32, x.data_ptr(), x.data_ptr(),
+                              1024, 512, 1, x.data_ptr(), x.data_ptr(), 16, None)
+    assert rc == _lib.ERR_WORKSPACE
+    assert L.mep_abi_version() == 1
