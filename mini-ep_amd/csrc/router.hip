@@ -5,10 +5,11 @@
 //     topk_logits, topk_idx = router_logits.topk(k, dim=-1)      (descending)
 //     topk_gate = softmax(topk_logits.float(), dim=-1).to(x.dtype)
 //
-// One wavefront owns 16 tokens.  The 16 x E logit tile is computed on the
-// matrix cores (bf16: v_mfma_f32_16x16x32_bf16, fp32: v_mfma_f32_16x16x4_f32)
-// with fp32 accumulation, x rows streamed straight from HBM into the MFMA A
-// operand and W_r read through the L1/L2 (64 KiB, shared by every wave).
+// One wavefront owns 16 tokens, four wavefronts share a workgroup and its LDS
+// copy of W_r.  The 16 x E logit tile is computed on the matrix cores (bf16:
+// v_mfma_f32_16x16x32_bf16, fp32: v_mfma_f32_16x16x4_f32) with fp32
+// accumulation; each wave issues all loads of its x rows for a K segment
+// before its first MFMA, so HBM latency is paid once per segment.
 // The tile then goes to LDS and every (token, expert) pair gets its rank
 //     rank(e) = #{e' : key(e') > key(e)  or  (key(e') == key(e) and e' < e)}
 // which is a total order: descending logits, lower expert id first among
@@ -32,105 +33,192 @@ __device__ __forceinline__ uint32_t order_key(float v) {
 }
 
 // Select the top-k of the `rows` x E fp32 tile in LDS (row stride `ld`) and
-// write topk_idx / gate for tokens t0 .. t0+rows-1.  Executed by one wave.
-// `sel_val` / `sel_idx` are LDS scratch of rows * k entries, `rsum` of rows.
-template <int GATE_DT>
-__device__ void select_topk_from_lds(const float* lg, int ld, int rows, int E, int k,
+// write topk_idx / gate for tokens t0 .. t0+rows-1.  Executed by one wave on its
+// own LDS slices; every wave of the workgroup calls it (it contains barriers).
+// Each logit gets the 64-bit key (order_key << 32) | ~e: unique per expert and
+// ordered exactly as "larger logit first, lower id among equals", so
+// rank(e) = #{j : key_j > key_e} -- one 64-bit compare and one add per j.
+// `keys` is LDS scratch of rows x kld 64-bit words (kld even), `sel_val` /
+// `sel_idx` rows * k entries, `rsum` rows.  EC is the expert count as a
+// compile-time constant (0 = runtime E, one key read at a time).
+template <int GATE_DT, int EC, int KC>
+__device__ void select_topk_from_lds(const float* lg, int ld, int rows, int E_rt, int k_rt,
                                      int64_t t0, int64_t n_tokens, float* sel_val,
                                      int* sel_idx, float* rsum, int64_t* topk_idx,
-                                     typename Elem<GATE_DT>::T* gate) {
+                                     typename Elem<GATE_DT>::T* gate, uint64_t* keys, int kld) {
   const int lane = lane_id();
+  const int E = EC > 0 ? EC : E_rt;
+  const int k = KC > 0 ? KC : k_rt;
   const int pairs = rows * E;
   for (int p = lane; p < pairs; p += 64) {
     const int t = p / E, e = p - t * E;
-    const float* row = lg + t * ld;
-    const uint32_t ke = order_key(row[e]);
+    keys[t * kld + e] = (static_cast<uint64_t>(order_key(lg[t * ld + e])) << 32) | static_cast<uint32_t>(~e);
+  }
+  __syncthreads();
+  for (int p = lane; p < pairs; p += 64) {
+    const int t = p / E, e = p - t * E;
+    const uint64_t* row = keys + t * kld;
+    const uint64_t ke = row[e];
     int rank = 0;
-    for (int j = 0; j < E; ++j) {
-      const uint32_t kj = order_key(row[j]);
-      rank += (kj > ke) | ((kj == ke) & (j < e));
+    if constexpr (EC > 0) {
+      uint64_t kv[EC];
+#pragma unroll
+      for (int j2 = 0; j2 < EC / 2; ++j2) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(row + 2 * j2);
+        kv[2 * j2] = (static_cast<uint64_t>(v.y) << 32) | v.x;
+        kv[2 * j2 + 1] = (static_cast<uint64_t>(v.w) << 32) | v.z;
+      }
+#pragma unroll
+      for (int j = 0; j < EC; ++j) rank += kv[j] > ke;
+    } else {
+      for (int j = 0; j < E; ++j) rank += row[j] > ke;
     }
     if (rank < k) {
-      sel_val[t * k + rank] = row[e];
+      sel_val[t * k + rank] = lg[t * ld + e];
       sel_idx[t * k + rank] = e;
     }
   }
   __syncthreads();
-  // softmax denominator per token, summed in slot order
-  for (int t = lane; t < rows; t += 64) {
-    const float m = sel_val[t * k];
-    float s = 0.0f;
-    for (int j = 0; j < k; ++j) s += expf(sel_val[t * k + j] - m);
-    rsum[t] = s;
-  }
-  __syncthreads();
-  for (int p = lane; p < rows * k; p += 64) {
-    const int t = p / k;
-    if (t0 + t >= n_tokens) continue;
-    const float g = expf(sel_val[p] - sel_val[t * k]) / rsum[t];
-    topk_idx[(t0 + t) * k + (p - t * k)] = sel_idx[p];
-    gate[(t0 + t) * k + (p - t * k)] = Elem<GATE_DT>::from_f32(g);
+  // softmax over each token's k selected logits, summed in slot order
+  if constexpr (KC > 0) {
+    // one lane per token: the k values in registers (16-byte LDS reads)
+    for (int t = lane; t < rows; t += 64) {
+      float v[KC];
+      if constexpr (KC % 4 == 0) {
+#pragma unroll
+        for (int q = 0; q < KC / 4; ++q) {
+          const f32x4 w4 = *reinterpret_cast<const f32x4*>(sel_val + t * KC + 4 * q);
+          v[4 * q] = w4.x; v[4 * q + 1] = w4.y; v[4 * q + 2] = w4.z; v[4 * q + 3] = w4.w;
+        }
+      } else {
+#pragma unroll
+        for (int q = 0; q < KC; ++q) v[q] = sel_val[t * KC + q];
+      }
+      float ex[KC], sum = 0.0f;
+#pragma unroll
+      for (int q = 0; q < KC; ++q) { ex[q] = expf(v[q] - v[0]); sum += ex[q]; }
+      if (t0 + t < n_tokens) {
+#pragma unroll
+        for (int q = 0; q < KC; ++q) {
+          topk_idx[(t0 + t) * KC + q] = sel_idx[t * KC + q];
+          gate[(t0 + t) * KC + q] = Elem<GATE_DT>::from_f32(ex[q] / sum);
+        }
+      }
+    }
+  } else {
+    for (int t = lane; t < rows; t += 64) {
+      const float m = sel_val[t * k];
+      float s = 0.0f;
+      for (int j = 0; j < k; ++j) s += expf(sel_val[t * k + j] - m);
+      rsum[t] = s;
+    }
+    __syncthreads();
+    for (int p = lane; p < rows * k; p += 64) {
+      const int t = p / k;
+      if (t0 + t >= n_tokens) continue;
+      const float g = expf(sel_val[p] - sel_val[t * k]) / rsum[t];
+      topk_idx[(t0 + t) * k + (p - t * k)] = sel_idx[p];
+      gate[(t0 + t) * k + (p - t * k)] = Elem<GATE_DT>::from_f32(g);
+    }
   }
 }
 
-// Logit tile of 16 tokens x (16*NF) experts on the matrix cores.
-// K is walked in blocks of 512 bytes per row; lane group g = lane/16 owns the
-// bytes [128g, 128g+128) of each block (8 chunks of 16 B).  Chunk j of every
-// group feeds MFMA step j; A and B use the same permutation of K, so the
-// accumulated dot products are unchanged.
-template <int DT, int NF>
-__global__ __launch_bounds__(64) void router_kernel(const typename Elem<DT>::T* __restrict__ x,
-                                                    const typename Elem<DT>::T* __restrict__ w,
-                                                    int64_t n_tokens, int hidden, int k,
-                                                    int64_t* __restrict__ topk_idx,
-                                                    typename Elem<DT>::T* __restrict__ gate,
-                                                    float* __restrict__ logits) {
+// Logit tiles on the matrix cores.  A workgroup of kWaves waves owns
+// kWaves x 16 tokens; W_r is staged through LDS in K segments of at most
+// kSegBytes (all waves share it), x is streamed straight from HBM into the
+// MFMA A operand with every load of a segment issued before its first MFMA.
+// K is walked in blocks of 512 bytes per row (32 chunks of 16 B); MFMA step j
+// of a block takes chunk 4j + g in lane group g = lane/16 (the MFMA's own K
+// order), so one load instruction reads 64 contiguous bytes of each of the 16
+// rows.  LDS rows of W are padded by 16 B, which spreads the 16 rows of a
+// fragment read over distinct banks.
+constexpr int kWaves = 4;
+constexpr int kSegBytes = 64 * 1024;
+
+template <int DT, int NF, int KC>
+__global__ __launch_bounds__(kWaves * 64) void router_kernel(const typename Elem<DT>::T* __restrict__ x,
+                                                             const typename Elem<DT>::T* __restrict__ w,
+                                                             int64_t n_tokens, int hidden, int k,
+                                                             int64_t* __restrict__ topk_idx,
+                                                             typename Elem<DT>::T* __restrict__ gate,
+                                                             float* __restrict__ logits) {
   typedef typename Elem<DT>::T T;
   constexpr int E = NF * 16;
-  constexpr int kElemsPerChunk = 16 / Elem<DT>::kBytes;   // 8 bf16 or 4 fp32
-  constexpr int kBlockElems = 32 * kElemsPerChunk;        // 4 groups x 8 chunks
-  __shared__ float lg[kRowsPerWave][E + 1];
-  __shared__ float sel_val[kRowsPerWave * 64];
-  __shared__ int sel_idx[kRowsPerWave * 64];
-  __shared__ float rsum[kRowsPerWave];
+  constexpr int EB = Elem<DT>::kBytes;
+  constexpr int kElemsPerChunk = 16 / EB;                 // 8 bf16 or 4 fp32
+  constexpr int kBlockElems = 32 * kElemsPerChunk;        // 4 groups x 8 chunks = 512 B
+  constexpr int kSegFit = (kSegBytes / (E * EB)) / kBlockElems * kBlockElems;
+  constexpr int kSegElems = kSegFit < 4 * kBlockElems ? kSegFit : 4 * kBlockElems;   // <= 4 K blocks of x in VGPRs
+  constexpr int kSegBlocks = kSegElems / kBlockElems;     // K blocks per segment
+  constexpr int kRowStride = kSegElems * EB + 16;         // padded LDS row of W (bytes)
+  static_assert(kSegBlocks >= 1 && kSegBlocks <= 4, "segment holds 1..4 K blocks");
+  __shared__ __attribute__((aligned(16))) unsigned char ws[E * kRowStride];
+  __shared__ float lg[kWaves][kRowsPerWave][E + 1];
+  __shared__ __attribute__((aligned(16))) uint64_t keys[kWaves][kRowsPerWave * (E + 2)];
+  __shared__ __attribute__((aligned(16))) float sel_val[kWaves][kRowsPerWave * 64];
+  __shared__ int sel_idx[kWaves][kRowsPerWave * 64];
+  __shared__ float rsum[kWaves][kRowsPerWave];
 
-  const int lane = lane_id();
+  const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
   const int r = lane & 15, g = lane >> 4;
-  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kRowsPerWave;
+  const int64_t t0 = (static_cast<int64_t>(blockIdx.x) * kWaves + wave) * kRowsPerWave;
   int64_t tok = t0 + r;
   if (tok >= n_tokens) tok = n_tokens - 1;   // in-bounds read, result discarded
-  const T* xrow = x + tok * hidden + g * (8 * kElemsPerChunk);
-  const T* wrow[NF];
-#pragma unroll
-  for (int nf = 0; nf < NF; ++nf) wrow[nf] = w + (nf * 16 + r) * hidden + g * (8 * kElemsPerChunk);
+  const T* xrow = x + tok * hidden + g * kElemsPerChunk;
 
   f32x4 acc[NF];
 #pragma unroll
   for (int nf = 0; nf < NF; ++nf) acc[nf] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int kb = 0; kb < hidden; kb += kBlockElems) {
-    u32x4 xa[8];
-    u32x4 wb[NF][8];
+  for (int seg = 0; seg < hidden; seg += kSegElems) {
+    const int nblk = (hidden - seg) / kBlockElems < kSegBlocks ? (hidden - seg) / kBlockElems : kSegBlocks;
+    // this wave's x for the segment, all loads in flight at once
+    u32x4 xa[kSegBlocks][8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) xa[j] = *reinterpret_cast<const u32x4*>(xrow + kb + j * kElemsPerChunk);
+    for (int b = 0; b < kSegBlocks; ++b)
+      if (b < nblk)
 #pragma unroll
-    for (int nf = 0; nf < NF; ++nf)
+        for (int j = 0; j < 8; ++j)
+          xa[b][j] = *reinterpret_cast<const u32x4*>(xrow + seg + b * kBlockElems + j * 4 * kElemsPerChunk);
+    // W_r[:, seg : seg + nblk*kBlockElems] -> LDS: every load of the segment is
+    // issued before the first LDS store (16-byte chunks, whole workgroup)
+    constexpr int kCpr = kSegElems / kElemsPerChunk;                   // chunks per W row
+    constexpr int kPerThread = E * kCpr / (kWaves * 64);
+    static_assert((E * kCpr) % (kWaves * 64) == 0, "W segment splits evenly");
+    const int live_cpr = nblk * kBlockElems / kElemsPerChunk;
+    u32x4 wt[kPerThread];
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        wb[nf][j] = *reinterpret_cast<const u32x4*>(wrow[nf] + kb + j * kElemsPerChunk);
+    for (int i = 0; i < kPerThread; ++i) {
+      const int c = tid + i * kWaves * 64, e = c / kCpr, q = c % kCpr;
+      if (q < live_cpr)
+        wt[i] = *reinterpret_cast<const u32x4*>(w + static_cast<int64_t>(e) * hidden + seg + q * kElemsPerChunk);
+    }
+    __syncthreads();                               // previous segment's readers are done
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int i = 0; i < kPerThread; ++i) {
+      const int c = tid + i * kWaves * 64, e = c / kCpr, q = c % kCpr;
+      if (q < live_cpr) *reinterpret_cast<u32x4*>(ws + e * kRowStride + q * 16) = wt[i];
+    }
+    __syncthreads();
 #pragma unroll
-      for (int nf = 0; nf < NF; ++nf) {
-        if constexpr (DT == MEP_DTYPE_BF16) {
-          acc[nf] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              __builtin_bit_cast(bf16x8, xa[j]), __builtin_bit_cast(bf16x8, wb[nf][j]), acc[nf], 0, 0, 0);
-        } else {
-          const float* xf = reinterpret_cast<const float*>(&xa[j]);
-          const float* wf = reinterpret_cast<const float*>(&wb[nf][j]);
+    for (int b = 0; b < kSegBlocks; ++b) {
+      if (b >= nblk) break;
 #pragma unroll
-          for (int q = 0; q < 4; ++q)
-            acc[nf] = __builtin_amdgcn_mfma_f32_16x16x4f32(xf[q], wf[q], acc[nf], 0, 0, 0);
+      for (int j = 0; j < 8; ++j) {
+#pragma unroll
+        for (int nf = 0; nf < NF; ++nf) {
+          const u32x4 wb = *reinterpret_cast<const u32x4*>(
+              ws + (nf * 16 + r) * kRowStride + (b * kBlockElems + (4 * j + g) * kElemsPerChunk) * EB);
+          if constexpr (DT == MEP_DTYPE_BF16) {
+            acc[nf] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                __builtin_bit_cast(bf16x8, xa[b][j]), __builtin_bit_cast(bf16x8, wb), acc[nf], 0, 0, 0);
+          } else {
+            const float* xf = reinterpret_cast<const float*>(&xa[b][j]);
+            const float* wf = reinterpret_cast<const float*>(&wb);
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              acc[nf] = __builtin_amdgcn_mfma_f32_16x16x4f32(xf[q], wf[q], acc[nf], 0, 0, 0);
+          }
         }
       }
     }
@@ -139,17 +227,17 @@ __global__ __launch_bounds__(64) void router_kernel(const typename Elem<DT>::T* 
 #pragma unroll
   for (int nf = 0; nf < NF; ++nf)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) lg[4 * g + i][nf * 16 + r] = acc[nf][i];
+    for (int i = 0; i < 4; ++i) lg[wave][4 * g + i][nf * 16 + r] = acc[nf][i];
   __syncthreads();
 
   if (logits != nullptr) {
     for (int p = lane; p < kRowsPerWave * E; p += 64) {
       const int t = p / E;
-      if (t0 + t < n_tokens) logits[(t0 + t) * E + (p - t * E)] = lg[t][p - t * E];
+      if (t0 + t < n_tokens) logits[(t0 + t) * E + (p - t * E)] = lg[wave][t][p - t * E];
     }
   }
-  select_topk_from_lds<DT>(&lg[0][0], E + 1, kRowsPerWave, E, k, t0, n_tokens, sel_val, sel_idx,
-                           rsum, topk_idx, gate);
+  select_topk_from_lds<DT, E, KC>(&lg[wave][0][0], E + 1, kRowsPerWave, E, k, t0, n_tokens, sel_val[wave],
+                                  sel_idx[wave], rsum[wave], topk_idx, gate, keys[wave], E + 2);
 }
 
 // Top-k + softmax of precomputed logits: one wave per `rows` tokens.
@@ -159,6 +247,7 @@ __global__ __launch_bounds__(64) void topk_softmax_kernel(const float* __restric
                                                           int64_t* __restrict__ topk_idx,
                                                           typename Elem<GATE_DT>::T* __restrict__ gate) {
   __shared__ float lg[1024 + 64];
+  __shared__ uint64_t keys[1024 + 64];
   __shared__ float sel_val[1024];
   __shared__ int sel_idx[1024];
   __shared__ float rsum[64];
@@ -170,24 +259,30 @@ __global__ __launch_bounds__(64) void topk_softmax_kernel(const float* __restric
     lg[t * ld + e] = (t0 + t < n_tokens) ? logits[(t0 + t) * E + e] : 0.0f;
   }
   __syncthreads();
-  select_topk_from_lds<GATE_DT>(lg, ld, rows, E, k, t0, n_tokens, sel_val, sel_idx, rsum,
-                                topk_idx, gate);
+  select_topk_from_lds<GATE_DT, 0, 0>(lg, ld, rows, E, k, t0, n_tokens, sel_val, sel_idx, rsum,
+                                      topk_idx, gate, keys, ld);
 }
 
 template <int DT>
 hipError_t launch_router(const void* x, const void* w, int64_t n, int hidden, int E, int k,
                          int64_t* idx, void* gate, float* logits, hipStream_t stream) {
   typedef typename Elem<DT>::T T;
-  const dim3 grid(static_cast<unsigned>((n + kRowsPerWave - 1) / kRowsPerWave));
+  const int per_block = kWaves * kRowsPerWave;
+  const dim3 grid(static_cast<unsigned>((n + per_block - 1) / per_block));
   const T* xp = static_cast<const T*>(x);
   const T* wp = static_cast<const T*>(w);
   T* gp = static_cast<T*>(gate);
+  // k = 8 (GraniteMoE's top-8) has a compile-time path; other k use the runtime one
+#define MEP_ROUTER_CASE(NF_)                                                                               \
+  if (k == 8) router_kernel<DT, NF_, 8><<<grid, kWaves * 64, 0, stream>>>(xp, wp, n, hidden, k, idx, gp, logits); \
+  else router_kernel<DT, NF_, 0><<<grid, kWaves * 64, 0, stream>>>(xp, wp, n, hidden, k, idx, gp, logits);
   switch (E) {
-    case 16: router_kernel<DT, 1><<<grid, 64, 0, stream>>>(xp, wp, n, hidden, k, idx, gp, logits); break;
-    case 32: router_kernel<DT, 2><<<grid, 64, 0, stream>>>(xp, wp, n, hidden, k, idx, gp, logits); break;
-    case 64: router_kernel<DT, 4><<<grid, 64, 0, stream>>>(xp, wp, n, hidden, k, idx, gp, logits); break;
+    case 16: MEP_ROUTER_CASE(1) break;
+    case 32: MEP_ROUTER_CASE(2) break;
+    case 64: MEP_ROUTER_CASE(4) break;
     default: return hipErrorInvalidValue;
   }
+#undef MEP_ROUTER_CASE
   return hipGetLastError();
 }
 

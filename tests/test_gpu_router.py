@@ -105,3 +105,16 @@ def test_router_rejects_bad_shapes():
         ops.router_topk(torch.randn(4, 256, device=DEV), torch.randn(48, 256, device=DEV), 8)
     idx, gate = ops.router_topk(torch.randn(0, 256, device=DEV), torch.randn(32, 256, device=DEV), 8)
     assert idx.shape == (0, 8)
+
+
+@pytest.mark.parametrize("k", [1, 4, 6])
+def test_router_fused_runtime_k(k):
+    """top-k other than 8 takes the router's runtime-k selection path."""
+    banner(f"router runtime k={k}")
+    g = torch.Generator().manual_seed(40 + k)
+    x = torch.randn(700, 1024, generator=g).to(torch.bfloat16)
+    w = (torch.randn(32, 1024, generator=g) * 0.02).to(torch.bfloat16)
+    idx, gate, logits = ops.router_topk(x.to(DEV), w.to(DEV), k, return_logits=True)
+    ridx, rgate = O.topk_softmax(to_np(logits), k, gate_bf16=True)
+    assert np.array_equal(to_np(idx), ridx)
+    assert np.abs(to_np(gate) - rgate).max() <= 2 ** -8
