@@ -76,6 +76,19 @@ __device__ __forceinline__ float silu_f(float v) {
 
 constexpr int pow2_floor(int v) { int r = 1; while (r * 2 <= v) r *= 2; return r; }
 
+// Workgroup barrier that orders LDS only: this wave's LDS reads and writes
+// complete (lgkmcnt(0)) before it arrives.  __syncthreads() also waits for
+// every outstanding global access (vmcnt(0)); in the epilogue that would wait
+// for the previous pass's stores and the next tile's first DMA stage.  The
+// empty asm statements keep the compiler from moving memory accesses across.
+constexpr int kLgkmcnt0 = 0xC07F;   // s_waitcnt lgkmcnt(0) alone (vmcnt 63, expcnt 7)
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(kLgkmcnt0);
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 template <int DT, class Cfg, bool GEMM1>
 __global__ __launch_bounds__(Cfg::NT) void grouped_gemm_kernel(GemmParams p) {
   typedef typename Elem<DT>::T T;
@@ -102,7 +115,7 @@ __global__ __launch_bounds__(Cfg::NT) void grouped_gemm_kernel(GemmParams p) {
   __shared__ __attribute__((aligned(16))) unsigned char smem[2 * STAGE + (2 * NLMAX + 2 + 2 * BM) * 4];
   int* const s_prefix = reinterpret_cast<int*>(smem + 2 * STAGE);   // [NLMAX + 1] tiles before expert j
   int* const s_off = s_prefix + NLMAX + 1;                          // [NLMAX + 1] row offsets
-  int* const s_rows = s_off + NLMAX + 1;                            // [2][BM] perm of the tile rows
+  int* const s_rows = s_off + NLMAX + 1;                            // [2][BM] perm of a tile's rows
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -120,7 +133,7 @@ __global__ __launch_bounds__(Cfg::NT) void grouped_gemm_kernel(GemmParams p) {
   if (tid == 0)
     for (int j = 0; j < nl; ++j) s_prefix[j + 1] += s_prefix[j];
   __syncthreads();
-  const int total = s_prefix[nl];
+  const int total = __builtin_amdgcn_readfirstlane(s_prefix[nl]);
   const int per_xcd = (total + 7) / 8;
   const int xcd = blockIdx.x % 8, slot = blockIdx.x / 8, nslots = gridDim.x / 8;
   const int n_my = slot < per_xcd ? (per_xcd - slot + nslots - 1) / nslots : 0;
@@ -137,12 +150,25 @@ __global__ __launch_bounds__(Cfg::NT) void grouped_gemm_kernel(GemmParams p) {
       if (s_prefix[mid] <= lt) lo = mid; else hi = mid - 1;
     }
     const int u = lt - s_prefix[lo];
-    Tile t;
-    t.e = lo;
-    t.row0 = s_off[lo] + (u / p.n_tiles_n) * BM;
-    t.row_end = s_off[lo + 1];
-    t.nt = u % p.n_tiles_n;
+    Tile t;                                        // uniform: keep it in SGPRs
+    t.e = __builtin_amdgcn_readfirstlane(lo);
+    t.row0 = __builtin_amdgcn_readfirstlane(s_off[lo] + (u / p.n_tiles_n) * BM);
+    t.row_end = __builtin_amdgcn_readfirstlane(s_off[lo + 1]);
+    t.nt = __builtin_amdgcn_readfirstlane(u % p.n_tiles_n);
     return t;
+  };
+
+  // ---- row maps: perm[row0 .. row0 + BM) of a tile DMA'd into LDS a tile
+  // ahead (clamped to the tile's last row, so every lane reads inside perm);
+  // GEMM-1 gathers its A rows through it, GEMM-2 scatters its output rows.
+  static_assert(BM % 64 == 0 && BM / 64 <= Cfg::NWAVES, "row-map DMA: one 64-row instruction per wave");
+  auto rowmap_dma = [&](const Tile& t, int parity) {
+    if (wave < BM / 64) {
+      const int r = min(t.row0 + wave * 64 + lane, t.row_end - 1);
+      __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)(p.perm + r),
+                                       (__attribute__((address_space(3))) void*)(s_rows + parity * BM + wave * 64),
+                                       4, 0, 0);
+    }
   };
 
   // ---- direct global -> LDS staging -------------------------------------------
@@ -154,11 +180,6 @@ __global__ __launch_bounds__(Cfg::NT) void grouped_gemm_kernel(GemmParams p) {
   uint32_t src_off[BPW];
   const unsigned char* g_base;
   auto setup = [&](const Tile& t, int parity) {
-    if constexpr (!GEMM1) {
-      // destinations of this tile's rows for the scatter epilogue
-      for (int r = tid; r < BM; r += NT)
-        s_rows[parity * BM + r] = (t.row0 + r < t.row_end) ? p.perm[t.row0 + r] : 0;
-    }
     // recompute the per-lane row terms here instead of keeping them live across
     // the whole tile loop (hoisted, they outgrow the register budget and spill)
     int lrow_v = lrow, lchunk_v = lchunk;
@@ -168,10 +189,9 @@ __global__ __launch_bounds__(Cfg::NT) void grouped_gemm_kernel(GemmParams p) {
 #pragma unroll
       for (int i = 0; i < BPW; ++i) {
         const int r = (wave * BPW + i) * 8 + lrow_v;
-        const int row = (t.row0 + r < t.row_end) ? t.row0 + r : t.row0;   // tail rows: any valid row
         int64_t src_row;
-        if constexpr (GEMM1) src_row = p.perm[row] / p.top_k;
-        else src_row = row;
+        if constexpr (GEMM1) src_row = s_rows[parity * BM + r] / p.top_k;       // gather (row map clamped)
+        else src_row = min(t.row0 + r, t.row_end - 1);                         // tail rows: any valid row
         src_off[i] = static_cast<uint32_t>((src_row * K + lchunk_v * EPC) * EB);
       }
     } else {
@@ -277,7 +297,7 @@ __global__ __launch_bounds__(Cfg::NT) void grouped_gemm_kernel(GemmParams p) {
           }
         }
       }
-      __syncthreads();
+      lds_barrier();
       for (int q = tid; q < BM * SCPR; q += NT) {
         const int r = q / SCPR, ch = q % SCPR;
         if (t.row0 + r >= t.row_end) continue;
@@ -287,7 +307,7 @@ __global__ __launch_bounds__(Cfg::NT) void grouped_gemm_kernel(GemmParams p) {
         dst += t.nt * CN + c0 + ch * EPC;
         *reinterpret_cast<u32x4*>(C + dst) = *reinterpret_cast<const u32x4*>(S + stage_addr(r, ch * 16));
       }
-      __syncthreads();
+      if (pass + 1 < NPASS) lds_barrier();
     }
   };
 
@@ -295,11 +315,16 @@ __global__ __launch_bounds__(Cfg::NT) void grouped_gemm_kernel(GemmParams p) {
   // Per tile: step kt computes from stage kt&1 while step kt+1 streams into the
   // other stage; each wave's vmcnt(0) plus the barrier publish it.  KT is even,
   // so the last step reads stage 1 and stage 0 is free for the next tile's
-  // first step, which streams in while this tile's epilogue drains via stage 1.
+  // first step, which streams in during that last step and while this tile's
+  // epilogue drains via stage 1.  The next tile's row map streams in during
+  // this tile's K loop.
   unsigned char* const stage0 = smem;
   unsigned char* const stage1 = smem + STAGE;
   const int KT = K / BKE;
   Tile cur = decode(tile_id(0));
+  rowmap_dma(cur, 0);
+  __builtin_amdgcn_s_waitcnt(kVmcnt0);
+  lds_barrier();
   setup(cur, 0);
   load_stage(0, stage0);
   for (int it = 0; tile_valid(it); ++it) {
@@ -308,19 +333,35 @@ __global__ __launch_bounds__(Cfg::NT) void grouped_gemm_kernel(GemmParams p) {
 #pragma unroll
       for (int j = 0; j < NF; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
     __builtin_amdgcn_s_waitcnt(kVmcnt0);
-    __syncthreads();
+    lds_barrier();
+    const bool has_next = tile_valid(it + 1);
+    Tile nxt = cur;
+    if (has_next) {
+      nxt = decode(tile_id(it + 1));
+      rowmap_dma(nxt, (it + 1) & 1);              // its buffer's last reader was the previous epilogue
+    }
     for (int kt = 0; kt < KT - 1; ++kt) {
       load_stage(kt + 1, (kt & 1) ? stage0 : stage1);
       compute((kt & 1) ? stage1 : stage0);
       __builtin_amdgcn_s_waitcnt(kVmcnt0);
-      __syncthreads();
+      lds_barrier();
+    }
+    // last step: stage 0 is free (barrier above).  The next tile's first step
+    // streams into it from here (GEMM-2) or from the end of this step (GEMM-1,
+    // whose gather setup would otherwise be live across the step's MFMAs and
+    // spill); either way the epilogue's staging writes wait for it, as the
+    // compiler makes LDS writes after an LDS DMA do.
+    const Tile done = cur;
+    if (!GEMM1 && has_next) {
+      cur = nxt;
+      setup(cur, (it + 1) & 1);
+      load_stage(0, stage0);
     }
     compute(stage1);
-    __syncthreads();                               // every wave is done with both stages
-    const Tile done = cur;
-    if (tile_valid(it + 1)) {
-      cur = decode(tile_id(it + 1));
-      setup(cur, (it + 1) & 1);
+    lds_barrier();                                 // every wave is done with stage 1
+    if (GEMM1 && has_next) {
+      cur = nxt;
+      setup(cur, (it + 1) & 1);                    // row map landed during the K loop
       load_stage(0, stage0);
     }
     epilogue(done, it & 1, stage1);
