@@ -18,14 +18,20 @@ clock, synchronised on both sides).  Per-stage durations come from HIP
 events on the stream the kernels run on; ``roofline`` is for GEMM-1, the
 dominant kernel (2/3 of the flops): 2*M*H*2I flops per launch over its mean
 event-timed duration vs the 2.5 PFLOP/s dense bf16 MFMA peak.
+``roofline.traffic`` is GEMM-1's HBM bytes per launch from the committed
+counter summary (``profiles/*hbm_traffic.md``: rocprofv3 FETCH_SIZE and
+WRITE_SIZE passes over this script, scaled by what the same counters read for
+the 256 MiB calibration copy this script issues before its warm-up), or null
+when that summary is absent.
 ``cpu_baseline`` times the numpy oracle on a bounded sample of the same
-workload on the host cores.
+workload on the host cores (and on one core).
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import re
 import sys
 import time
 from pathlib import Path
@@ -48,32 +54,52 @@ def parse_args(argv=None):
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--tokens", type=int, default=16384)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-sample-tokens", type=int, default=4096)
+    ap.add_argument("--cpu-sample-tokens", type=int, default=16384)
+    ap.add_argument("--cpu-single-thread-tokens", type=int, default=4096)
     return ap.parse_args(argv)
 
 
-def cpu_baseline(layer, tokens: int) -> dict:
+def cpu_baseline(layer, tokens: int, single_tokens: int) -> dict:
     """The numpy oracle (router + LocalMoEBackend restatement, fp32) on the
-    first `tokens` tokens of the workload, on the host cores."""
+    first `tokens` tokens of the workload on the host cores (at most 16
+    threads), and on the first `single_tokens` tokens on one thread."""
     import numpy as np
+    import torch
     from threadpoolctl import threadpool_limits
 
     from oracle import moe_oracle as O
 
     cores = max(1, min(len(os.sched_getaffinity(0)), 16))
-    x = layer.x[:tokens].to(__import__("torch").bfloat16).float().numpy()
-    wr = layer.w_router.to(__import__("torch").bfloat16).float().numpy()
-    wi = layer.w_in.to(__import__("torch").bfloat16).float().numpy()
-    wo = layer.w_out.to(__import__("torch").bfloat16).float().numpy()
-    with threadpool_limits(limits=cores):
-        t0 = time.perf_counter()
-        idx, gate = O.topk_softmax(O.router_logits(x, wr), layer.top_k)
-        out = O.moe_layer_local(x, idx, gate, wi, wo)
-        dt = time.perf_counter() - t0
-    assert np.isfinite(out).all()
+    x = layer.x.to(torch.bfloat16).float().numpy()
+    wr = layer.w_router.to(torch.bfloat16).float().numpy()
+    wi = layer.w_in.to(torch.bfloat16).float().numpy()
+    wo = layer.w_out.to(torch.bfloat16).float().numpy()
+
+    def run(n: int, threads: int) -> float:
+        with threadpool_limits(limits=threads):
+            t0 = time.perf_counter()
+            idx, gate = O.topk_softmax(O.router_logits(x[:n], wr), layer.top_k)
+            out = O.moe_layer_local(x[:n], idx, gate, wi, wo)
+            dt = time.perf_counter() - t0
+        assert np.isfinite(out).all()
+        return dt
+
+    dt = run(tokens, cores)
+    dt1 = run(single_tokens, 1)
     return {"value": tokens / dt, "unit": "tokens/s", "cores": cores, "kind": "port",
             "sample": f"first {tokens} of the {layer.x.shape[0]} tokens, fp32 numpy oracle "
-                      f"(router + LocalMoEBackend restatement), {dt:.2f} s"}
+                      f"(router + LocalMoEBackend restatement), {cores} threads, {dt:.2f} s",
+            "single_thread": {"value": single_tokens / dt1, "unit": "tokens/s", "cores": 1,
+                              "sample": f"first {single_tokens} tokens, 1 thread, {dt1:.2f} s"}}
+
+
+def traffic_from_profile() -> dict | None:
+    """GEMM-1 HBM bytes per launch from the committed counter summary, if any."""
+    for f in sorted((ROOT / "profiles").glob("*hbm_traffic.md")):
+        m = re.search(r"traffic_bytes_per_launch\s*=\s*([0-9.eE+]+)", f.read_text())
+        if m:
+            return {"bytes": float(m.group(1)), "source": f"profiles/{f.name}"}
+    return None
 
 
 def main(argv=None) -> int:
@@ -127,6 +153,14 @@ def main(argv=None) -> int:
             ev[5].record()
         return disp
 
+    # calibration copy of known size for the HBM counters (FETCH_SIZE /
+    # WRITE_SIZE of this copy scale the kernels' counters to bytes)
+    cal_src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+    cal_dst = torch.empty_like(cal_src)
+    cal_dst.copy_(cal_src)
+    torch.cuda.synchronize()
+    del cal_src, cal_dst
+
     # routing statistics of the workload (outside any timed region)
     disp = step()
     torch.cuda.synchronize()
@@ -170,6 +204,7 @@ def main(argv=None) -> int:
     }
     gemm_util = (flops_g1 + flops_g2) / (g1_s + g2_s) / PEAK_BF16_FLOPS
     achieved = flops_g1 / g1_s / 1e12
+    traffic = traffic_from_profile()
     res = {
         "metric": METRIC,
         "value": T / (ms_step / 1e3),
@@ -190,12 +225,15 @@ def main(argv=None) -> int:
         "layer_tflops": (flops_g1 + flops_g2) / (ms_step / 1e3) / 1e12,
         "roofline": {"kernel": "grouped_gemm_kernel GEMM-1 (gate/up + SwiGLU)", "bound": "mfma",
                      "achieved": achieved, "peak": PEAK_BF16_FLOPS / 1e12, "unit": "TFLOP/s",
-                     "frac": achieved * 1e12 / PEAK_BF16_FLOPS, "traffic": None,
+                     "frac": achieved * 1e12 / PEAK_BF16_FLOPS,
+                     "traffic": traffic["bytes"] if traffic else None,
+                     "traffic_source": traffic["source"] if traffic else None,
                      "flops_per_launch": flops_g1, "mean_launch_ms": stage_ms["gemm1_swiglu"]},
         "stages": detail,
     }
     if not args.no_cpu_baseline:
-        res["cpu_baseline"] = cpu_baseline(layer, min(args.cpu_sample_tokens, T))
+        res["cpu_baseline"] = cpu_baseline(layer, min(args.cpu_sample_tokens, T),
+                                           min(args.cpu_single_thread_tokens, T))
     print(json.dumps(res), flush=True)
     return 0
 
