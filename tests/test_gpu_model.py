@@ -1,0 +1,127 @@
+"""Config 3: 24-layer GraniteMoE-shaped bf16 model (hidden 1024, 16 q / 8 kv
+heads of 64, RoPE, RMSNorm, vocab 49155, 32 experts top-8 per layer), seeded
+random-init weights, prefill 8 x 512 seeded random token ids, then 32 greedy
+steps with every MoE block on the HIP kernels.
+
+Expert weights are drawn N(0, 0.05) (input_linear) and N(0, 0.1)
+(output_linear) so that every MoE block moves the residual stream by O(1).
+With N(0, 0.02) everywhere, or (0.03, 0.05) for the experts, the random model
+only repeats its input token, its greedy choices do not depend on the MoE
+blocks at all, and identity would hold trivially.  The test shows that they
+do depend on them here: scaling one layer's MoE output by 0.9 changes a
+fifth of the decoded tokens or more.
+
+Greedy identity.  The torch restatement of the reference MoE (router +
+LocalMoEBackend, same bf16 rounding points) is teacher-forced on the HIP
+model's tokens, decision by decision.  A random 24-layer model whose MoE
+blocks matter is chaotic: one-ulp bf16 rounding differences in the expert
+outputs, which the HIP path and the reference legitimately have (their fp32
+sums run in different orders), grow through the layers and flip decisions
+whose top-2 logit gap is small.  The bar is therefore the model's own noise
+floor: the HIP path may differ from the reference in at most as many
+decisions as the reference differs from itself when +-1 ulp is injected into
+~40 % of its MoE outputs (max over 2 seeds, at least 4), and only where the
+reference's top-2 gap is below MARGIN.
+"""
+import time
+
+import pytest
+import torch
+
+from helpers import banner
+from miniep_amd.model import GraniteMoeModel, ModelConfig, build_hip_model, greedy_generate, layer_keys, random_weights
+from torch_moe_ref import TorchMoERef, torch_route
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+EXPERT_STD = (0.05, 0.1)
+MARGIN = 0.1
+
+
+class _Scaled:
+    """A MoE backend whose output is scaled (the sensitivity probe)."""
+
+    def __init__(self, inner, factor):
+        self.inner, self.factor = inner, factor
+
+    def __call__(self, *a, **kw):
+        return self.inner(*a, **kw) * self.factor
+
+
+class _UlpNoise:
+    """A MoE backend whose output gets +-1 bf16 ulp on ~40 % of its elements."""
+
+    def __init__(self, inner, seed):
+        self.inner = inner
+        self.g = torch.Generator(device=DEV).manual_seed(seed)
+
+    def __call__(self, *a, **kw):
+        y = self.inner(*a, **kw)
+        yf = y.float()
+        ulp = torch.ldexp(torch.ones_like(yf), torch.frexp(yf)[1] - 8)
+        hit = torch.rand(yf.shape, generator=self.g, device=DEV) < 0.4
+        sign = torch.where(torch.rand(yf.shape, generator=self.g, device=DEV) < 0.5, -1.0, 1.0)
+        return (yf + hit * sign * ulp).to(y.dtype)
+
+
+def _ref_model(cfg, w, wrap=lambda i, b: b):
+    return GraniteMoeModel(cfg, w, torch_route,
+                           [wrap(i, TorchMoERef(w[layer_keys(i)["w_in"]], w[layer_keys(i)["w_out"]]))
+                            for i in range(cfg.num_hidden_layers)])
+
+
+def test_config3_greedy_identity():
+    banner("config 3: 24-layer model, prefill 8x512, 32 greedy steps")
+    cfg = ModelConfig()
+    w = random_weights(cfg, seed=0, dtype=torch.bfloat16, device=DEV, expert_std=EXPERT_STD)
+    hip = build_hip_model(cfg, w, check=True)
+    ref = _ref_model(cfg, w)
+    g = torch.Generator().manual_seed(1)
+    prompts = torch.randint(1, cfg.vocab_size, (8, 512), generator=g).to(DEV)
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    toks, _ = greedy_generate(hip, prompts, 32)
+    torch.cuda.synchronize()
+    t_hip = time.perf_counter() - t0
+    rtoks, rmargins = greedy_generate(ref, prompts, 32, forced=toks)
+    differ = toks != rtoks
+    n_differ = int(differ.sum())
+
+    # the model's own noise floor: the reference against itself with +-1 ulp MoE noise
+    ref_free, _ = greedy_generate(ref, prompts, 32)
+    floor = 0
+    for seed in range(2):
+        noisy = _ref_model(cfg, w, lambda i, b: _UlpNoise(b, 1000 * seed + i))
+        ntoks, _ = greedy_generate(noisy, prompts, 32, forced=ref_free)
+        floor = max(floor, int((ntoks != ref_free).sum()))
+
+    # sensitivity: the decisions depend on the MoE blocks
+    ref.moe[12] = _Scaled(ref.moe[12], 0.9)
+    ptoks, _ = greedy_generate(ref, prompts, 32)
+    moved = int((ptoks != ref_free).sum())
+
+    print(f"HIP model: prefill + 32 steps in {t_hip:.2f} s; decisions differing from the reference "
+          f"{n_differ}/{toks.numel()} (top-2 gaps there {[round(float(x), 4) for x in rmargins[differ]]}); "
+          f"reference noise floor {floor}/{toks.numel()}; free-running sequences identical "
+          f"{int((toks == ref_free).all(1).sum())}/8; layer-12 MoE x0.9 moves {moved}/{toks.numel()}", flush=True)
+    assert moved > toks.numel() // 5, "the decoded tokens do not depend on the MoE blocks"
+    assert n_differ <= max(floor, 4), "HIP path differs from the reference beyond the model's noise floor"
+    assert bool((rmargins[differ] < MARGIN).all()), "a decision differs away from a near-tie"
+    assert int(toks.min()) >= 0 and int(toks.max()) < cfg.vocab_size
+
+
+def test_config3_prefill_logits_close():
+    banner("config 3: prefill logits vs torch reference (4 layers)")
+    cfg = ModelConfig(num_hidden_layers=4)
+    w = random_weights(cfg, seed=2, dtype=torch.bfloat16, device=DEV, expert_std=EXPERT_STD)
+    hip = build_hip_model(cfg, w)
+    ref = _ref_model(cfg, w)
+    g = torch.Generator().manual_seed(3)
+    ids = torch.randint(1, cfg.vocab_size, (2, 256), generator=g).to(DEV)
+    at = torch.full((2,), 255, device=DEV)
+    a, b = hip(ids, logits_at=at), ref(ids, logits_at=at)
+    err = float((a - b).abs().max() / b.abs().max())
+    print(f"last-position logits rel err {err:.3e}", flush=True)
+    assert err < 2e-2
+    assert torch.equal(a.argmax(-1), b.argmax(-1))
