@@ -181,6 +181,35 @@ int mep_combine(const void* y_entries, const void* topk_gate, const int32_t* row
                 const uint8_t* valid_mask, int64_t n_tokens, int32_t top_k,
                 int32_t hidden, int32_t dtype, void* out, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Expert-parallel send side (one GPU's part; the all-to-all itself is the
+ * caller's collective).
+ *
+ * mep_gather_rows: the send buffer, x_flat[token_ids[order]] (ep.py:226):
+ *   out[i, :] = x[perm[i] / top_k, :]   for i < n_rows
+ * and, when topk_idx / ids_out are given, the experts that travel with them
+ * (ep.py:225, flat_expert[order]): ids_out[i] = topk_idx_flat[perm[i]].
+ * `perm` is the destination-sorted entry order, i.e. mep_dispatch run over
+ * `dest` as the key (world-1 tables, n_experts = world): its `counts` are the
+ * send counts (ep.py:222) and its `row_of_entry` the inverse order (ep.py:239).
+ *   x (N, H)  perm (n_rows,) int32  topk_idx (N*k,) int64 or NULL
+ *   ids_out (n_rows,) int64 or NULL  out (n_rows, H)
+ *
+ * mep_combine_rows: the return path, gated = back[inv] * gate followed by
+ * scatter_combine (ep.py:237-242):
+ *   out[t] = sum_{s, row_of_entry[t*k+s] >= 0} gate[t,s] * y_rows[row_of_entry[t*k+s]]
+ * in slot order in fp32 (the same reduction as mep_combine, rows read
+ * through row_of_entry).
+ *   y_rows (rows, H)  topk_gate (N, k)  row_of_entry (N*k,) int32  out (N, H)
+ * ---------------------------------------------------------------------- */
+int mep_gather_rows(const void* x, int64_t n_tokens, int32_t top_k, const int32_t* perm,
+                    int64_t n_rows, int32_t hidden, int32_t dtype, const int64_t* topk_idx,
+                    int64_t* ids_out, void* out, void* stream);
+
+int mep_combine_rows(const void* y_rows, const void* topk_gate, const int32_t* row_of_entry,
+                     const uint8_t* valid_mask, int64_t n_tokens, int32_t top_k,
+                     int32_t hidden, int32_t dtype, void* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

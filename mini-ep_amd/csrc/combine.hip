@@ -9,6 +9,13 @@
 // reduction: each thread owns 16 bytes of one token's output row, loads the
 // k cells of that token (k x 16 B, all in flight), and sums gate * y in slot
 // order in fp32 -- the same fixed order on every run, no atomics.
+//
+// The expert-parallel return path (ep.py:237-242: inv[order] = arange,
+// gated = back[inv] * gate, scatter_combine) is the same reduction with the
+// (token, slot) row read through `row_of_entry` (the inverse of the
+// destination sort): mep_combine_rows.  Its send-buffer counterpart,
+// mep_gather_rows (ep.py:226, x_flat[token_ids[order]]), copies the rows of x
+// in send order.
 #include "common.h"
 
 namespace mep {
@@ -18,7 +25,7 @@ constexpr int kThreads = 256;
 constexpr int kMaxK = 32;
 constexpr int kStage = 1024;   // staged (token, slot) cells per block
 
-template <int DT>
+template <int DT, bool INDEXED>
 __global__ __launch_bounds__(kThreads) void combine_kernel(const typename Elem<DT>::T* __restrict__ y,
                                                            const typename Elem<DT>::T* __restrict__ gate,
                                                            const int32_t* __restrict__ row_of_entry,
@@ -31,6 +38,7 @@ __global__ __launch_bounds__(kThreads) void combine_kernel(const typename Elem<D
   const int tokens_per_block = kThreads / tpt;
   __shared__ float s_gate[kStage];                      // [tokens_per_block * k]
   __shared__ uint8_t s_here[kStage];
+  __shared__ int32_t s_row[INDEXED ? kStage : 1];       // row of each cell (indexed form)
   const int tid = threadIdx.x;
   const int local_tok = tid / tpt;
   const int c = tid - local_tok * tpt;
@@ -47,6 +55,7 @@ __global__ __launch_bounds__(kThreads) void combine_kernel(const typename Elem<D
     }
     s_gate[i] = g;
     s_here[i] = here;
+    if constexpr (INDEXED) s_row[i] = here ? row_of_entry[t * k + i % k] : 0;
   }
   __syncthreads();
   const int64_t t = tok0 + local_tok;
@@ -60,7 +69,10 @@ __global__ __launch_bounds__(kThreads) void combine_kernel(const typename Elem<D
   for (int s = 0; s < k; ++s) {
     if (!s_here[local_tok * k + s]) continue;           // cell computed elsewhere / invalid token
     const float g = s_gate[local_tok * k + s];
-    const u32x4 v = *reinterpret_cast<const u32x4*>(ybase + static_cast<int64_t>(s) * hidden);
+    const T* ycell;
+    if constexpr (INDEXED) ycell = y + static_cast<int64_t>(s_row[local_tok * k + s]) * hidden + c * EPC;
+    else ycell = ybase + static_cast<int64_t>(s) * hidden;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(ycell);
     if constexpr (DT == MEP_DTYPE_BF16) {
       const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
@@ -90,6 +102,63 @@ __global__ __launch_bounds__(kThreads) void combine_kernel(const typename Elem<D
   *reinterpret_cast<u32x4*>(out + t * hidden + c * EPC) = o;
 }
 
+// out[i, :] = x[perm[i] / top_k, :] (and ids_out[i] = topk_flat[perm[i]]):
+// one thread per 16 bytes of an output row.
+template <int DT>
+__global__ __launch_bounds__(kThreads) void gather_rows_kernel(const typename Elem<DT>::T* __restrict__ x,
+                                                               const int32_t* __restrict__ perm,
+                                                               int64_t n_rows, int top_k, int hidden,
+                                                               const int64_t* __restrict__ topk_flat,
+                                                               int64_t* __restrict__ ids_out,
+                                                               typename Elem<DT>::T* __restrict__ out) {
+  constexpr int EPC = 16 / Elem<DT>::kBytes;
+  const int cpr = hidden / EPC;                         // 16-byte chunks per row
+  const int64_t q = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  const int64_t i = q / cpr;
+  if (i >= n_rows) return;
+  const int c = static_cast<int>(q - i * cpr);
+  const int32_t f = perm[i];
+  const int64_t src = f / top_k;
+  *reinterpret_cast<u32x4*>(out + i * hidden + c * EPC) =
+      *reinterpret_cast<const u32x4*>(x + src * hidden + c * EPC);
+  if (ids_out != nullptr && c == 0) ids_out[i] = topk_flat[f];
+}
+
+template <bool INDEXED>
+int combine_entry(const char* fn, const void* y, const void* topk_gate, const int32_t* row_of_entry,
+                  const uint8_t* valid_mask, int64_t n_tokens, int32_t top_k, int32_t hidden, int32_t dtype,
+                  void* out, void* stream) {
+  clear_error();
+  MEP_REQUIRE(dtype == MEP_DTYPE_F32 || dtype == MEP_DTYPE_BF16, MEP_ERR_INVALID_ARG,
+              "%s: unknown dtype %d", fn, dtype);
+  MEP_REQUIRE(n_tokens >= 0 && top_k >= 1 && top_k <= kMaxK, MEP_ERR_INVALID_ARG,
+              "%s: bad n_tokens / top_k %d", fn, top_k);
+  const int epc = 16 / dtype_bytes(dtype);
+  MEP_REQUIRE(hidden > 0 && hidden % epc == 0 && hidden / epc <= kThreads &&
+                  kThreads % (hidden / epc) == 0,
+              MEP_ERR_UNSUPPORTED, "%s: hidden %d unsupported for this dtype", fn, hidden);
+  MEP_REQUIRE(kThreads / (hidden / epc) * top_k <= kStage, MEP_ERR_UNSUPPORTED,
+              "%s: hidden %d too small for top_k %d", fn, hidden, top_k);
+  if (n_tokens == 0) return MEP_OK;
+  MEP_REQUIRE(y && topk_gate && row_of_entry && out, MEP_ERR_INVALID_ARG, "%s: null pointer", fn);
+  MEP_REQUIRE((reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(out)) % 16 == 0,
+              MEP_ERR_INVALID_ARG, "%s: y / out must be 16-byte aligned", fn);
+  const int tokens_per_block = kThreads / (hidden / epc);
+  const dim3 grid(static_cast<unsigned>((n_tokens + tokens_per_block - 1) / tokens_per_block));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == MEP_DTYPE_BF16)
+    combine_kernel<MEP_DTYPE_BF16, INDEXED><<<grid, kThreads, 0, s>>>(
+        static_cast<const uint16_t*>(y), static_cast<const uint16_t*>(topk_gate), row_of_entry,
+        valid_mask, n_tokens, top_k, hidden, static_cast<uint16_t*>(out));
+  else
+    combine_kernel<MEP_DTYPE_F32, INDEXED><<<grid, kThreads, 0, s>>>(
+        static_cast<const float*>(y), static_cast<const float*>(topk_gate), row_of_entry,
+        valid_mask, n_tokens, top_k, hidden, static_cast<float*>(out));
+  hipError_t e = hipGetLastError();
+  MEP_REQUIRE(e == hipSuccess, MEP_ERR_HIP, "%s: launch failed: %s", fn, hipGetErrorString(e));
+  return MEP_OK;
+}
+
 }  // namespace
 }  // namespace mep
 
@@ -98,33 +167,45 @@ using namespace mep;
 extern "C" int mep_combine(const void* y_entries, const void* topk_gate, const int32_t* row_of_entry,
                            const uint8_t* valid_mask, int64_t n_tokens, int32_t top_k, int32_t hidden,
                            int32_t dtype, void* out, void* stream) {
+  return combine_entry<false>("mep_combine", y_entries, topk_gate, row_of_entry, valid_mask, n_tokens, top_k,
+                              hidden, dtype, out, stream);
+}
+
+extern "C" int mep_combine_rows(const void* y_rows, const void* topk_gate, const int32_t* row_of_entry,
+                                const uint8_t* valid_mask, int64_t n_tokens, int32_t top_k, int32_t hidden,
+                                int32_t dtype, void* out, void* stream) {
+  return combine_entry<true>("mep_combine_rows", y_rows, topk_gate, row_of_entry, valid_mask, n_tokens, top_k,
+                             hidden, dtype, out, stream);
+}
+
+extern "C" int mep_gather_rows(const void* x, int64_t n_tokens, int32_t top_k, const int32_t* perm,
+                               int64_t n_rows, int32_t hidden, int32_t dtype, const int64_t* topk_idx,
+                               int64_t* ids_out, void* out, void* stream) {
   clear_error();
   MEP_REQUIRE(dtype == MEP_DTYPE_F32 || dtype == MEP_DTYPE_BF16, MEP_ERR_INVALID_ARG,
-              "mep_combine: unknown dtype %d", dtype);
-  MEP_REQUIRE(n_tokens >= 0 && top_k >= 1 && top_k <= kMaxK, MEP_ERR_INVALID_ARG,
-              "mep_combine: bad n_tokens / top_k %d", top_k);
+              "mep_gather_rows: unknown dtype %d", dtype);
+  MEP_REQUIRE(n_tokens >= 0 && n_rows >= 0 && top_k >= 1 && n_rows <= n_tokens * top_k, MEP_ERR_INVALID_ARG,
+              "mep_gather_rows: bad sizes");
   const int epc = 16 / dtype_bytes(dtype);
-  MEP_REQUIRE(hidden > 0 && hidden % epc == 0 && hidden / epc <= kThreads &&
-                  kThreads % (hidden / epc) == 0,
-              MEP_ERR_UNSUPPORTED, "mep_combine: hidden %d unsupported for this dtype", hidden);
-  MEP_REQUIRE(kThreads / (hidden / epc) * top_k <= kStage, MEP_ERR_UNSUPPORTED,
-              "mep_combine: hidden %d too small for top_k %d", hidden, top_k);
-  if (n_tokens == 0) return MEP_OK;
-  MEP_REQUIRE(y_entries && topk_gate && row_of_entry && out, MEP_ERR_INVALID_ARG,
-              "mep_combine: null pointer");
-  MEP_REQUIRE((reinterpret_cast<uintptr_t>(y_entries) | reinterpret_cast<uintptr_t>(out)) % 16 == 0,
-              MEP_ERR_INVALID_ARG, "mep_combine: y_entries / out must be 16-byte aligned");
-  const int tokens_per_block = kThreads / (hidden / epc);
-  const dim3 grid(static_cast<unsigned>((n_tokens + tokens_per_block - 1) / tokens_per_block));
+  MEP_REQUIRE(hidden > 0 && hidden % epc == 0, MEP_ERR_UNSUPPORTED,
+              "mep_gather_rows: hidden %d is not a multiple of %d", hidden, epc);
+  MEP_REQUIRE((ids_out == nullptr) == (topk_idx == nullptr), MEP_ERR_INVALID_ARG,
+              "mep_gather_rows: topk_idx and ids_out go together");
+  if (n_rows == 0) return MEP_OK;
+  MEP_REQUIRE(x && perm && out, MEP_ERR_INVALID_ARG, "mep_gather_rows: null pointer");
+  MEP_REQUIRE((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(out)) % 16 == 0,
+              MEP_ERR_INVALID_ARG, "mep_gather_rows: x / out must be 16-byte aligned");
+  const int64_t chunks = n_rows * (hidden / epc);
+  const dim3 grid(static_cast<unsigned>((chunks + kThreads - 1) / kThreads));
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == MEP_DTYPE_BF16)
-    combine_kernel<MEP_DTYPE_BF16><<<grid, kThreads, 0, s>>>(
-        static_cast<const uint16_t*>(y_entries), static_cast<const uint16_t*>(topk_gate), row_of_entry,
-        valid_mask, n_tokens, top_k, hidden, static_cast<uint16_t*>(out));
+    gather_rows_kernel<MEP_DTYPE_BF16><<<grid, kThreads, 0, s>>>(static_cast<const uint16_t*>(x), perm, n_rows,
+                                                                top_k, hidden, topk_idx, ids_out,
+                                                                static_cast<uint16_t*>(out));
   else
-    combine_kernel<MEP_DTYPE_F32><<<grid, kThreads, 0, s>>>(
-        static_cast<const float*>(y_entries), static_cast<const float*>(topk_gate), row_of_entry,
-        valid_mask, n_tokens, top_k, hidden, static_cast<float*>(out));
-  MEP_CHECK_LAUNCH("mep_combine");
+    gather_rows_kernel<MEP_DTYPE_F32><<<grid, kThreads, 0, s>>>(static_cast<const float*>(x), perm, n_rows,
+                                                               top_k, hidden, topk_idx, ids_out,
+                                                               static_cast<float*>(out));
+  MEP_CHECK_LAUNCH("mep_gather_rows");
   return MEP_OK;
 }

@@ -9,11 +9,13 @@ miniep/ep.py, miniep/balancer.py) over the C ABI of ``include/miniep_amd.h``:
   ops: router_topk, topk_softmax, dispatch, grouped_swiglu, combine
 """
 from . import _lib, ops
-from .backend import EmulatedEPMoEBackend, EPStats, HipEPShareBackend, HipMoEBackend, route
+from .backend import (EmulatedEPExchangeBackend, EmulatedEPMoEBackend, EPStats, HipEPShareBackend,
+                      HipMoEBackend, SendBatch, route)
 from .balancer import plan_balanced
 from .placement import Placement
 
 __all__ = [
+    "EmulatedEPExchangeBackend", "SendBatch",
     "_lib", "ops", "route", "HipMoEBackend", "HipEPShareBackend", "EmulatedEPMoEBackend",
     "EPStats", "Placement", "plan_balanced",
 ]

@@ -70,6 +70,10 @@ _SIGNATURES = {
                                        _c_void_p, _i32, _i32, _i32, _c_void_p, _c_void_p]),
     "mep_combine": (ctypes.c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i32,
                                    _i32, _i32, _c_void_p, _c_void_p]),
+    "mep_gather_rows": (ctypes.c_int, [_c_void_p, _i64, _i32, _c_void_p, _i64, _i32, _i32, _c_void_p,
+                                       _c_void_p, _c_void_p, _c_void_p]),
+    "mep_combine_rows": (ctypes.c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i32,
+                                        _i32, _i32, _c_void_p, _c_void_p]),
 }
 
 _LIB = None

@@ -17,6 +17,8 @@ Block.forward (:192-195).  This module provides:
 """
 from __future__ import annotations
 
+from dataclasses import dataclass
+
 import torch
 
 from . import ops
@@ -142,12 +144,110 @@ class HipEPShareBackend:
             self.stats.recv_tokens_per_layer[self.layer] += disp.offsets[-1].to(torch.long)
         return disp
 
+    def send(self, x_flat, topk_idx, valid_mask=None, rr=None) -> "SendBatch":
+        """Sender half of EPMoEBackend.__call__ (ep.py:216-226) for this rank's
+        own tokens: route_counts, destinations with this rank's round-robin
+        counters `rr` (1, E) (zeros = after reset_rr), the destination-sorted
+        order (stable), the send counts per rank, the inverse order, and the
+        send buffer (rows of x and their experts) in that order."""
+        n, k = topk_idx.shape
+        dev = self.w_in.device
+        E = self.placement.num_experts
+        world = self.placement.world
+        table, n_rep = self.placement.tables(self.layer, dev)
+        has_rep = self.placement.has_replicas(self.layer)
+        if has_rep and rr is None:
+            rr = torch.zeros(1, E, dtype=torch.long, device=dev)
+        rc = self.stats.route_counts[self.layer] if self.stats is not None else None
+        nobody = torch.full((E,), -1, dtype=torch.int32, device=dev)
+        d = ops.dispatch(topk_idx, valid_mask, E, table, n_rep, has_rep, rr if has_rep else None, -1,
+                         nobody, 0, route_counts=rc, want_dest=True, check=self.check)
+        # the destination-sorted order is the dispatch itself keyed by destination
+        key = d.dest[: n * k].clamp(min=0).view(n, k).to(torch.int64)   # masked entries stay masked
+        t1, r1, ident = _world1_tables(world, dev)
+        srt = ops.dispatch(key, valid_mask, world, t1, r1, False, None, 0, ident, world, check=False)
+        m = int(srt.offsets[-1])
+        send_x, send_ids = ops.gather_rows(x_flat.to(self.w_in.dtype), srt.perm, m, k, topk_idx)
+        return SendBatch(send_x, send_ids, srt.counts, srt.row_of_entry, m)
+
+    def receive(self, recv_x, recv_experts) -> torch.Tensor:
+        """Receiver half (ep.py:228-231): the rows that arrived, one expert each,
+        through this rank's resident experts; outputs in arrival order.  A row
+        for an expert not resident here raises NotResidentError (ep.py:230)."""
+        n = recv_x.shape[0]
+        dev = self.w_in.device
+        if n == 0:
+            return torch.empty(0, recv_x.shape[1], dtype=self.w_in.dtype, device=dev)
+        E = self.placement.num_experts
+        t1, r1, _ = _world1_tables(E, dev)
+        d = ops.dispatch(recv_experts.view(n, 1), None, E, t1, r1, False, None, 0, self.g2l,
+                         len(self.local_experts), check=self.check)
+        if self.stats is not None:
+            self.stats.recv_tokens_per_layer[self.layer] += d.offsets[-1].to(torch.long)
+        return ops.grouped_swiglu(recv_x.to(self.w_in.dtype), d, self.w_in, self.w_out)
+
     def share(self, x_flat, topk_idx, valid_mask=None, seg_tokens=None, rr=None, y_entries=None,
               want_dest=False):
         """(Dispatch, y_entries): this rank's rows and their expert outputs."""
         disp = self.dispatch(topk_idx, valid_mask, seg_tokens, rr, want_dest)
         y = ops.grouped_swiglu(x_flat.to(self.w_in.dtype), disp, self.w_in, self.w_out, y_entries)
         return disp, y
+
+
+@dataclass
+class SendBatch:
+    """What one rank sends: rows (m, H) and their experts (m,) grouped by
+    destination rank, `send_counts` (world,) rows per destination, and `inv`
+    (N*k,) the row of each of its entries in the send order (-1 if masked)."""
+    x: torch.Tensor
+    experts: torch.Tensor
+    send_counts: torch.Tensor
+    inv: torch.Tensor
+    rows: int
+
+
+class EmulatedEPExchangeBackend:
+    """EPMoEBackend.__call__ (ep.py:210-249) end to end for `world` ranks on one
+    GPU, each rank with its own weight slice: every rank routes its own tokens
+    (source segment r of the batch), builds its send buffer (``send``), the
+    two all-to-alls are device copies between the ranks' buffers in rank
+    order (what all_to_all_single with these split sizes delivers), each
+    rank runs what it received (``receive``), and each sender combines the
+    returned rows through its inverse order (ops.combine_rows).  Equal to
+    HipMoEBackend bit for bit for any placement (ep.py:1-8)."""
+
+    def __init__(self, layer: int, placement: Placement, world: int, w_in_full: torch.Tensor,
+                 w_out_full: torch.Tensor, stats: "EPStats | None" = None, check: bool = True):
+        self.layer, self.placement, self.world = layer, placement, world
+        self.ranks = [HipEPShareBackend(layer, placement, r, w_in_full[ids], w_out_full[ids], stats=stats,
+                                        check=check)
+                      for r, ids in ((r, placement.experts_of_rank(r)[layer]) for r in range(world))]
+
+    def __call__(self, x_flat, topk_idx, topk_gate, valid_mask=None, seg_tokens=None, rr=None):
+        n = x_flat.shape[0]
+        seg = [n * r // self.world for r in range(self.world + 1)] if seg_tokens is None else list(seg_tokens)
+        sl = [slice(seg[r], seg[r + 1]) for r in range(self.world)]
+        vm = [None if valid_mask is None else valid_mask[s] for s in sl]
+        sends = [be.send(x_flat[s], topk_idx[s], vm[r], None if rr is None else rr[r:r + 1])
+                 for r, (be, s) in enumerate(zip(self.ranks, sl))]
+        # counts exchange (ep.py:120-124): per sender, the row offsets of each destination
+        off = [[0] + torch.cumsum(b.send_counts, 0).tolist() for b in sends]
+        # all_to_all of rows and experts (ep.py:224-226), then the experts of each rank
+        ys = []
+        for q, be in enumerate(self.ranks):
+            rx = torch.cat([b.x[off[r][q]:off[r][q + 1]] for r, b in enumerate(sends)])
+            re = torch.cat([b.experts[off[r][q]:off[r][q + 1]] for r, b in enumerate(sends)])
+            ys.append(be.receive(rx, re))
+        # the reverse all_to_all (ep.py:233) and each sender's combine (ep.py:237-242)
+        recv_off = [[0] + torch.cumsum(torch.tensor([off[r][q + 1] - off[r][q] for r in range(self.world)]),
+                                       0).tolist() for q in range(self.world)]
+        outs = []
+        for r, b in enumerate(sends):
+            back = torch.cat([ys[q][recv_off[q][r]:recv_off[q][r + 1]] for q in range(self.world)])
+            if back.shape[0] == 0:
+                back = torch.zeros(1, x_flat.shape[1], dtype=ys[0].dtype, device=x_flat.device)
+            outs.append(ops.combine_rows(back, topk_gate[sl[r]], b.inv, vm[r]))
+        return torch.cat(outs)
 
 
 class EmulatedEPMoEBackend:

@@ -258,3 +258,39 @@ def combine(y_entries: torch.Tensor, topk_gate: torch.Tensor, row_of_entry: torc
                                 n, k, h, _dtype_code(y_entries), out.data_ptr(), _stream(dev))
     _lib.check(rc, "mep_combine")
     return out
+
+
+def combine_rows(y_rows: torch.Tensor, topk_gate: torch.Tensor, row_of_entry: torch.Tensor,
+                 valid_mask: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Expert-parallel return path (ep.py:237-242): out[t] = sum over present
+    slots s (slot order) of gate[t,s] * y_rows[row_of_entry[t*k+s]]."""
+    dev = _require_device(y_rows, topk_gate, row_of_entry, out)
+    n, k = topk_gate.shape
+    h = y_rows.shape[1]
+    gate = topk_gate.to(y_rows.dtype).contiguous()
+    vm = _mask_u8(valid_mask, n)
+    if out is None:
+        out = torch.empty((n, h), dtype=y_rows.dtype, device=dev)
+    rc = _lib.lib().mep_combine_rows(y_rows.data_ptr(), gate.data_ptr(), row_of_entry.data_ptr(), _ptr(vm),
+                                     n, k, h, _dtype_code(y_rows), out.data_ptr(), _stream(dev))
+    _lib.check(rc, "mep_combine_rows")
+    return out
+
+
+def gather_rows(x: torch.Tensor, perm: torch.Tensor, n_rows: int, top_k: int,
+                topk_idx: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """Send buffer of expert parallelism (ep.py:225-226): rows x[perm[i] // top_k]
+    for i < n_rows, and with `topk_idx` the expert of each row."""
+    dev = _require_device(x, perm, topk_idx)
+    x = x.contiguous()
+    n, h = x.shape
+    out = torch.empty((n_rows, h), dtype=x.dtype, device=dev)
+    ids = None
+    flat = None
+    if topk_idx is not None:
+        flat = topk_idx.reshape(-1).to(torch.int64).contiguous()
+        ids = torch.empty(n_rows, dtype=torch.int64, device=dev)
+    rc = _lib.lib().mep_gather_rows(x.data_ptr(), n, top_k, perm.data_ptr(), n_rows, h, _dtype_code(x),
+                                    _ptr(flat), _ptr(ids), out.data_ptr(), _stream(dev))
+    _lib.check(rc, "mep_gather_rows")
+    return out, ids

@@ -39,6 +39,11 @@ class Placement:
         self._dev_tables: dict = {}
         self._rr = torch.zeros(self.num_layers, self.num_experts, dtype=torch.long, device=self.device)
 
+    @property
+    def world(self) -> int:
+        """Ranks the placement spans: 1 + the highest rank holding an expert."""
+        return 1 + max(r for layer in self.owners for o in layer for r in o)
+
     @staticmethod
     def _build_table(owners_l):
         """table[e, j] = rank of e's j-th replica, unused cells 0 (ep.py:35-45)."""
