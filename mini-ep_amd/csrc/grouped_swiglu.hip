@@ -33,6 +33,8 @@
 // tile's first K step is already streaming into the other.
 #include "common.h"
 
+#include <type_traits>
+
 namespace mep {
 namespace {
 
@@ -66,7 +68,22 @@ struct GemmParams {
   int K;                     // reduction length
   int N;                     // output columns (GEMM-1: I; GEMM-2: H)
   int n_tiles_n;             // column tiles per row tile
+  uint32_t a_bytes;          // size of A in bytes (< 4 GiB)
+  uint32_t k_magic;          // entry / top_k == umulhi(entry, k_magic) >> k_shift for entry < 2^31
+  int k_shift;
 };
+
+// Round-up reciprocal for exact division by d of every n < 2^31: with
+// s = ceil(log2 d) and m = ceil(2^(31+s) / d) (< 2^32 for d >= 2),
+// n / d == (n * m) >> (31 + s) == umulhi(n, m) >> (s - 1).  d == 1 is
+// flagged by m = 0 (the quotient is n).
+void div_magic(uint32_t d, uint32_t* magic, int* shift) {
+  if (d <= 1) { *magic = 0; *shift = 0; return; }
+  int s = 0;
+  while ((uint64_t(1) << s) < d) ++s;
+  *magic = static_cast<uint32_t>(((uint64_t(1) << (31 + s)) + d - 1) / d);
+  *shift = s - 1;
+}
 
 // silu(v) = v / (1 + e^-v) with the hardware exp2 and reciprocal (about 1 ulp
 // each); saturates correctly: v -> -inf gives -0, v -> +inf gives v.
@@ -385,6 +402,392 @@ hipError_t launch(const GemmParams& p, int64_t max_rows, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// ============================================================================
+// bf16 path: 8 waves, 4-stage LDS ring, AGPR accumulators.
+//
+// Tile 256 x 256 (GEMM-1: 128 gate + 128 up columns), 8 waves (4 x 2) of
+// 64 x 128.  K moves 32 bf16 (64 B per row) per step through a ring of four
+// 32 KiB LDS stages filled by global_load_lds_dwordx4 three steps ahead of the
+// MFMAs that consume them; the ring runs on across tile boundaries, so the
+// next tile's first three steps stream in while this tile's last steps and its
+// epilogue run.  During step s each wave
+//   - issues its 4 DMA blocks of step s+3 (one per group of 8 MFMAs),
+//   - reads the fragments of step s+1 (3 ds_read_b128 per group) into the
+//     other register set,
+//   - runs the 32 MFMAs of step s on the fragments read during step s-1,
+// then waits for step s+2's DMA (vmcnt) and joins an LDS-only barrier.
+// The MFMAs are inline asm with "+a" accumulators: the compiler keeps the
+// 128 accumulators in AGPRs and does not shuffle them between register
+// files (with the builtin it does, and spills).  Measured on the K loop alone
+// (streamed A rows): this schedule beats the two-stage 128 B/row loop by
+// about 15 %.
+//
+// Epilogue: stage s_last % 4 is free between the last step of a tile and the
+// next step (its fragments were read during step s_last - 1 and the next DMA
+// into it is issued at step s_last + 1), so the output is staged through it in
+// passes of 64 columns x 256 rows (128-byte rows XOR-swizzled by r & 7) and
+// stored with 16-byte coalesced stores.  The K order of a tile is rotated by
+// its column-tile index (n_tile * KT / 4 steps), which spreads the tiles that
+// run at the same time over more HBM / L2 channels; the rotation depends on
+// the output columns only, so every output element is summed in the same
+// order wherever its row sits in the dispatch.
+namespace bfk {
+constexpr int BM = 256, BN = 256, NT = 512, NW = 8;
+constexpr int RB = 64;                        // bytes per row per step
+constexpr int KS = RB / 2;                    // bf16 elements per step
+constexpr int STEP = (BM + BN) * RB;          // 32 KiB per stage
+constexpr int NSTAGE = 4;
+constexpr int ASTAGE = BM * RB;                    // A rows of one stage (16 KiB); the weight rows take as much
+static_assert(BN * RB == ASTAGE, "A and weight rows of a stage are the same size");
+constexpr int BREGION = NSTAGE * ASTAGE;           // weight rows of all stages start here (64 KiB)
+constexpr int MF = 4, NF = 8;                 // 16 x 16 fragments per wave (64 x 128)
+constexpr int BPW = 4;                        // 1 KiB DMA blocks (16 rows x 64 B) per wave per step
+constexpr int NLMAX = 256;
+constexpr int LDS_BYTES = NSTAGE * STEP + (2 * (NLMAX + 1) + 2 * BM) * 4;
+// buffer resource word 3 for raw 32-bit buffer access on gfx9-family parts
+constexpr int kBufWord3 = 0x00020000;
+static_assert(BPW == MF, "one DMA block per MFMA group");
+static_assert((BM + BN) / 16 == NW * BPW, "DMA blocks cover the stage");
+}  // namespace bfk
+
+// 16x16x32 bf16 MFMA with the accumulator pinned to AGPRs; src0 = weight
+// fragment, src1 = row fragment, so the result is C^T (lane: one row, 4
+// consecutive columns).  ZERO starts a new accumulation (C operand 0).
+__device__ __forceinline__ void mfma_acc(f32x4& acc, const u32x4& w, const u32x4& a) {
+  asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(w), "v"(a));
+}
+__device__ __forceinline__ void mfma_first(f32x4& acc, const u32x4& w, const u32x4& a) {
+  asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, 0" : "=a"(acc) : "v"(w), "v"(a));
+}
+// Orders later reads of `acc` after every earlier volatile asm (an empty asm
+// that claims to rewrite it).  AMDGPU constraints live in device functions
+// only: in a kernel body the host pass would parse "a" as an x86 register.
+__device__ __forceinline__ void pin_acc(f32x4& acc) { asm volatile("" : "+a"(acc)); }
+// buffer_load_dwordx4 ... lds of one 1 KiB block: lane L's 16 bytes from
+// base + voff + soff land at lds + 16 L; an offset at or past `bytes` reads
+// zeros instead of faulting.  (A plain device function: inside the kernel
+// template the host pass drops the kernel's launch stub.)
+__device__ __forceinline__ void buffer_lds_16(const unsigned char* base, int bytes, uint32_t voff, int soff,
+                                              unsigned char* lds) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(base), 0, bytes, bfk::kBufWord3),
+      (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
+}
+
+template <bool GEMM1>
+__global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
+  using namespace bfk;
+  __shared__ __attribute__((aligned(16))) unsigned char smem[LDS_BYTES];
+  int* const s_prefix = reinterpret_cast<int*>(smem + NSTAGE * STEP);   // [NLMAX + 1] tiles before expert j
+  int* const s_off = s_prefix + NLMAX + 1;                             // [NLMAX + 1] row offsets
+  int* const s_rows = s_off + NLMAX + 1;                               // [2][BM] row maps
+
+  const int tid = threadIdx.x;
+  // wave index as a scalar: keeps per-wave choices (A or weight rows, buffer
+  // resources) in SGPRs
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int K = p.K;
+  const int KT = K / KS;                      // steps per tile (even, >= 4, multiple of 4)
+  const int nl = p.n_local;
+
+  // ---- tile table ---------------------------------------------------------------
+  for (int j = tid; j <= nl; j += NT) s_off[j] = p.offsets[j];
+  __syncthreads();
+  for (int j = tid; j < nl; j += NT)
+    s_prefix[j + 1] = ((s_off[j + 1] - s_off[j] + BM - 1) / BM) * p.n_tiles_n;
+  if (tid == 0) s_prefix[0] = 0;
+  __syncthreads();
+  if (tid == 0)
+    for (int j = 0; j < nl; ++j) s_prefix[j + 1] += s_prefix[j];
+  __syncthreads();
+  const int total = __builtin_amdgcn_readfirstlane(s_prefix[nl]);
+  const int per_xcd = (total + 7) / 8;
+  const int xcd = blockIdx.x % 8, slot = blockIdx.x / 8, nslots = gridDim.x / 8;
+  const int n_my = slot < per_xcd ? (per_xcd - slot + nslots - 1) / nslots : 0;
+  auto tile_id = [&](int i) { return xcd * per_xcd + slot + i * nslots; };
+  auto tile_valid = [&](int i) { return i < n_my && tile_id(i) < total; };
+  if (!tile_valid(0)) return;
+
+  struct Tile { int e, row0, row_end, nt; };
+  auto decode = [&](int lt) {
+    int lo = 0, hi = nl - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (s_prefix[mid] <= lt) lo = mid; else hi = mid - 1;
+    }
+    const int u = lt - s_prefix[lo];
+    Tile t;
+    t.e = __builtin_amdgcn_readfirstlane(lo);
+    t.row0 = __builtin_amdgcn_readfirstlane(s_off[lo] + (u / p.n_tiles_n) * BM);
+    t.row_end = __builtin_amdgcn_readfirstlane(s_off[lo + 1]);
+    t.nt = __builtin_amdgcn_readfirstlane(u % p.n_tiles_n);
+    return t;
+  };
+  auto rowmap_dma = [&](const Tile& t, int parity) {
+    if (wave < BM / 64) {
+      const int r = min(t.row0 + wave * 64 + lane, t.row_end - 1);
+      __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)(p.perm + r),
+                                       (__attribute__((address_space(3))) void*)(s_rows + parity * BM + wave * 64),
+                                       4, 0, 0);
+    }
+  };
+
+  // ---- DMA sources ----------------------------------------------------------------
+  // Block q = wave * BPW + i holds stage rows 16q .. 16q+15 (A rows 0..255, then
+  // weight rows); lane L moves 16 B of row 16q + L/4 into byte 16 L of the
+  // block, i.e. physical chunk L & 3, and fetches logical chunk
+  // (L & 3) ^ ((row >> 1) & 3): 64-byte rows XOR-swizzled by (r >> 1) & 3,
+  // which makes the fragment reads conflict-free.
+  const bool wave_a = wave < 4;
+  // Output columns of a weight stage row.  Within each aligned group of 32
+  // rows (two 16-column fragments j, j+1), fragment row n of fragment j2 holds
+  // column 8 (n / 4) + 4 j2 + n % 4: lane group lg then owns columns
+  // 8 lg .. 8 lg + 7 of the group across the two fragments (16 contiguous
+  // bytes of bf16 output per lane and store).
+  auto pair_cols = [](int rb) { return (rb & ~31) | (((rb & 15) >> 2) << 3) | (((rb >> 4) & 1) << 2) | (rb & 3); };
+  // (base, bytes) rather than a buffer resource: a struct member of type
+  // __amdgpu_buffer_rsrc_t makes the host pass drop the kernel's launch stub
+  struct Src { const unsigned char* base; int bytes; uint32_t off[BPW]; int rot; };
+  auto setup = [&](const Tile& t, int parity) {
+    int lrow = lane >> 2, lchunk = (lane & 3) ^ ((lane >> 3) & 3);
+    asm volatile("" : "+v"(lrow), "+v"(lchunk));
+    Src s;
+    s.rot = (KT % 4 == 0) ? (t.nt * (KT / 4)) % KT : 0;
+    if (wave_a) {
+      s.base = static_cast<const unsigned char*>(p.A);
+      s.bytes = static_cast<int>(p.a_bytes);
+#pragma unroll
+      for (int i = 0; i < BPW; ++i) {
+        const int r = (wave * BPW + i) * 16 + lrow;
+        int64_t src_row;
+        if constexpr (GEMM1) {
+          const uint32_t f = static_cast<uint32_t>(s_rows[parity * BM + r]);   // flat entry t*k + s
+          src_row = p.k_magic ? (__umulhi(f, p.k_magic) >> p.k_shift) : f;
+        }
+        else src_row = min(t.row0 + r, t.row_end - 1);
+        s.off[i] = static_cast<uint32_t>((src_row * K + lchunk * 8) * 2);
+      }
+    } else {
+      s.base = static_cast<const unsigned char*>(p.W) + static_cast<int64_t>(t.e) * p.w_expert_stride * 2;
+      s.bytes = static_cast<int>(p.w_expert_stride * 2);
+#pragma unroll
+      for (int i = 0; i < BPW; ++i) {
+        const int rb = (wave * BPW + i) * 16 + lrow - BM;
+        int wrow;
+        if constexpr (GEMM1) wrow = (rb < BN / 2) ? t.nt * (BN / 2) + pair_cols(rb) : p.N + t.nt * (BN / 2) + pair_cols(rb - BN / 2);
+        else wrow = t.nt * BN + pair_cols(rb);
+        s.off[i] = static_cast<uint32_t>((static_cast<int64_t>(wrow) * K + lchunk * 8) * 2);
+      }
+    }
+    return s;
+  };
+  // per-lane 32-bit offset, the K position in the scalar offset
+  // LDS layout: the A rows of stage s at s * 16 KiB, its weight rows at
+  // 64 KiB + s * 16 KiB, so every fragment read of the ring is one of two
+  // base registers plus an immediate below 64 KiB
+  const int lds_blk = wave_a ? wave * BPW * 1024 : BREGION + (wave - 4) * BPW * 1024;
+  auto dma_blk = [&](const Src& s, int kt, int stage, int i) {
+    int kd = kt + s.rot;
+    if (kd >= KT) kd -= KT;
+    buffer_lds_16(s.base, s.bytes, s.off[i], kd * RB, smem + lds_blk + stage * ASTAGE + i * 1024);
+  };
+
+  // ---- fragments ------------------------------------------------------------------
+  const int lr = lane & 15, lg = lane >> 4;
+  const uint32_t cpo = static_cast<uint32_t>((lg ^ ((lr >> 1) & 3)) << 4);
+  const uint32_t a_lane = static_cast<uint32_t>((wm * 64 + lr) * RB) + cpo;
+  uint32_t b_lo, b_hi;   // GEMM-1: gate / up fragment rows; GEMM-2: one contiguous range
+  if constexpr (GEMM1) {
+    b_lo = static_cast<uint32_t>(BREGION + (wn * 64 + lr) * RB) + cpo;
+    b_hi = static_cast<uint32_t>(BREGION + (BN / 2 + wn * 64 + lr) * RB) + cpo;
+  } else {
+    b_lo = static_cast<uint32_t>(BREGION + (wn * 128 + lr) * RB) + cpo;
+    b_hi = b_lo + 4 * 16 * RB;
+  }
+  auto b_addr = [&](int j) { return (j < 4 ? b_lo + j * 16 * RB : b_hi + (j - 4) * 16 * RB); };
+  // Row fragments are double-buffered (fa[set]); weight fragments are not: the
+  // MFMAs run column-major (group j = the 4 MFMAs that use weight fragment j),
+  // so fb[j] is refilled with the next step's fragment right after group j.
+  // (An MFMA reads its A/B operands when it issues.)  64 fragment VGPRs.
+  u32x4 fa[2][MF], fb[NF];
+  f32x4 acc[MF][NF];
+
+  // One step: MFMAs on fa[SET] / fb (read during the previous step); with DMA,
+  // issue the 4 blocks of step dkt of the tile `s` describes into stage
+  // dstage (one every other group); with RD, read the next step's fragments
+  // from stage rstage.  ZERO starts the accumulation.
+  auto step = [&](auto set_c, auto zero_c, auto dma_c, auto rd_c, const Src& s, int dkt, int dstage, int rstage) {
+    constexpr int SET = decltype(set_c)::value;
+    constexpr bool ZERO = decltype(zero_c)::value, DMA = decltype(dma_c)::value, RD = decltype(rd_c)::value;
+    const unsigned char* R = smem + rstage * ASTAGE;
+#pragma unroll
+    for (int j = 0; j < NF; ++j) {
+      if constexpr (DMA) {
+        if (j % 2 == 0) dma_blk(s, dkt, dstage, j / 2);
+      }
+#pragma unroll
+      for (int i = 0; i < MF; ++i) {
+        if constexpr (ZERO) mfma_first(acc[i][j], fb[j], fa[SET][i]);
+        else mfma_acc(acc[i][j], fb[j], fa[SET][i]);
+      }
+      if constexpr (RD) {
+        fb[j] = *reinterpret_cast<const u32x4*>(R + b_addr(j));
+        if (j % 2 == 1) fa[SET ^ 1][j / 2] = *reinterpret_cast<const u32x4*>(R + a_lane + (j / 2) * 16 * RB);
+      }
+      asm volatile("" ::: "memory");
+    }
+    // publish: the DMA of step (this step + 2) has landed, every read of this
+    // step is done.  vmcnt(BPW) suffices whatever else is outstanding (the
+    // previous epilogue's stores): loads complete in order, and this step's
+    // BPW DMA blocks were issued after step+2's.
+    if constexpr (DMA) __builtin_amdgcn_s_waitcnt(0x0F70 | BPW);
+    else __builtin_amdgcn_s_waitcnt(kVmcnt0);
+    lds_barrier();
+  };
+
+  // ---- epilogue -----------------------------------------------------------------------
+  // Straight from the accumulators to global memory: with the weight rows
+  // permuted per 32-column group (pair_cols), lane (lr, lg) of the fragment
+  // pair (2 jp, 2 jp + 1) in row fragment i holds 8 consecutive output columns
+  // of one row: one 16-byte store (16 rows x 64 contiguous bytes per
+  // instruction).  No LDS staging and no barrier: the stores drain while the
+  // next tile's MFMAs run.
+  typedef uint16_t T;
+  T* const C = static_cast<T*>(p.C);
+  constexpr int CN = GEMM1 ? BN / 2 : BN;     // output columns per tile
+  auto epilogue = [&](const Tile& t, int parity) {
+    // the last MFMAs' results must be written before the AGPRs are read (the
+    // asm hides the MFMAs from the hazard recognizer): pad, then tie every
+    // accumulator to an (empty) asm after the padding so no read moves above it
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < MF; ++i)
+#pragma unroll
+      for (int j = 0; j < NF; ++j) pin_acc(acc[i][j]);
+    // per-lane terms from an opaque copy of the thread index, so the compiler
+    // cannot hoist them out of the tile loop (they would be spilled there)
+    int et = tid;
+    asm volatile("" : "+v"(et));
+    const int elr = et & 15, elg = (et >> 4) & 3;
+    const int col = t.nt * CN + (GEMM1 ? wn * 64 : wn * 128) + elg * 8;   // first column of fragment pair 0
+#pragma unroll
+    for (int i = 0; i < MF; ++i) {
+      const int r = wm * 64 + i * 16 + elr;
+      int64_t row;
+      if constexpr (GEMM1) row = t.row0 + r;
+      else row = s_rows[parity * BM + r];                                   // (token, slot) cell
+      T* const dst = C + row * p.N + col;
+      const bool ok = t.row0 + r < t.row_end;
+#pragma unroll
+      for (int jp = 0; jp < (GEMM1 ? NF / 4 : NF / 2); ++jp) {             // fragment pairs (2 jp, 2 jp + 1)
+        float v[8];
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int j = 2 * jp + h;
+            v[4 * h + q] = GEMM1 ? silu_f(acc[i][j][q]) * acc[i][j + NF / 2][q] : acc[i][j][q];
+          }
+        u32x4 w;
+#pragma unroll
+        for (int h = 0; h < 4; ++h) w[h] = pack_bf16x2(v[2 * h], v[2 * h + 1]);
+        if (ok) *reinterpret_cast<u32x4*>(dst + jp * 32) = w;
+      }
+    }
+  };
+
+  // ---- persistent step loop ---------------------------------------------------------
+  // Invariant at the start of step kt of a tile: stages kt%4 and (kt+1)%4 hold
+  // their data (waited + barrier), the fragments of step kt are in register set
+  // kt&1, the DMA of step kt+2 is in flight.  Steps of consecutive tiles share
+  // the ring; KT % 4 == 0, so step kt of every tile uses stage kt % 4.
+  Tile cur = decode(tile_id(0));
+  bool has_next = tile_valid(1);
+  Tile nxt = has_next ? decode(tile_id(1)) : cur;
+  rowmap_dma(cur, 0);
+  if (has_next) rowmap_dma(nxt, 1);
+  __builtin_amdgcn_s_waitcnt(kVmcnt0);
+  lds_barrier();
+  Src sc = setup(cur, 0);
+#pragma unroll
+  for (int g = 0; g < BPW; ++g) dma_blk(sc, 0, 0, g);
+#pragma unroll
+  for (int g = 0; g < BPW; ++g) dma_blk(sc, 1, 1, g);
+  __builtin_amdgcn_s_waitcnt(kVmcnt0);
+  lds_barrier();
+#pragma unroll
+  for (int g = 0; g < BPW; ++g) dma_blk(sc, 2, 2, g);
+  // fragments of a tile's step 0 (stage 0): read at the tile start, after the
+  // previous epilogue, so no fragment registers are live across an epilogue
+  auto first_frags = [&]() {
+#pragma unroll
+    for (int g = 0; g < MF; ++g) fa[0][g] = *reinterpret_cast<const u32x4*>(smem + a_lane + g * 16 * RB);
+#pragma unroll
+    for (int j = 0; j < NF; ++j) fb[j] = *reinterpret_cast<const u32x4*>(smem + b_addr(j));
+    __builtin_amdgcn_s_waitcnt(kLgkmcnt0);
+  };
+
+  std::integral_constant<int, 0> S0;
+  std::integral_constant<int, 1> S1;
+  std::integral_constant<bool, false> NO;
+  std::integral_constant<bool, true> YES;
+  for (int it = 0;; ++it) {
+    first_frags();
+    // steps are unrolled by four so every stage offset is an immediate: step
+    // kt reads stage (kt+1)&3 and DMAs into stage (kt+3)&3
+    step(S0, YES, YES, YES, sc, 3, 3, 1);
+    // every wave is past its previous epilogue (barrier above), so the row
+    // map buffer that epilogue read can take the next tile's row map; it
+    // lands by the end of step 1 and is read by setup() at step KT-3
+    if (it > 0 && has_next) rowmap_dma(nxt, (it + 1) & 1);
+    step(S1, NO, YES, YES, sc, 4, 0, 2);
+    step(S0, NO, YES, YES, sc, 5, 1, 3);
+    step(S1, NO, YES, YES, sc, 6, 2, 0);
+    // steady state: steps 4m .. 4m+3 DMA steps 4m+3 .. 4m+6 of this tile
+    for (int k4 = 4; k4 < KT - 4; k4 += 4) {
+      step(S0, NO, YES, YES, sc, k4 + 3, 3, 1);
+      step(S1, NO, YES, YES, sc, k4 + 4, 0, 2);
+      step(S0, NO, YES, YES, sc, k4 + 5, 1, 3);
+      step(S1, NO, YES, YES, sc, k4 + 6, 2, 0);
+    }
+    // last four steps: KT-4 DMAs this tile's last step, the other three the
+    // next tile's steps 0..2.  Without a next tile they re-read this tile's
+    // steps 0..2 (in bounds, never consumed) so the code has no branch here.
+    step(S0, NO, YES, YES, sc, KT - 1, 3, 1);
+    sc = has_next ? setup(nxt, (it + 1) & 1) : setup(cur, it & 1);   // next row map landed during step 0
+    step(S1, NO, YES, YES, sc, 0, 0, 2);
+    step(S0, NO, YES, YES, sc, 1, 1, 3);
+    step(S1, NO, YES, NO, sc, 2, 2, 0);
+    epilogue(cur, it & 1);
+    if (!has_next) {
+      // no DMA may still be writing this workgroup's LDS when its waves end
+      __builtin_amdgcn_s_waitcnt(kVmcnt0);
+      break;
+    }
+    cur = nxt;
+    has_next = tile_valid(it + 2);
+    if (has_next) nxt = decode(tile_id(it + 2));
+  }
+}
+
+template <bool GEMM1>
+hipError_t launch_bf16(const GemmParams& p, int64_t max_rows, hipStream_t stream) {
+  static int n_cu = 0;
+  if (n_cu == 0) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n_cu <= 0)
+      n_cu = 256;
+  }
+  int64_t tiles = ((max_rows + bfk::BM - 1) / bfk::BM + p.n_local) * p.n_tiles_n;
+  if (tiles == 0) return hipSuccess;
+  int64_t grid = tiles < n_cu ? tiles : n_cu;
+  grid = (grid + 7) / 8 * 8;
+  moe_gemm_bf16_kernel<GEMM1><<<dim3(static_cast<unsigned>(grid)), bfk::NT, 0, stream>>>(p);
+  return hipGetLastError();
+}
+
 // Tile shapes: bf16 256x256 (GEMM-1: 128 gate + 128 up columns) on 8 waves
 // (4 x 2, 64 x 128 per wave, 2 waves per SIMD, no spills); fp32 128x128 on
 // 4 waves.
@@ -392,15 +795,19 @@ typedef TileCfg<256, 256, 4, 2> CfgBf16;
 typedef TileCfg<128, 128, 2, 2> CfgF32;
 
 template <int DT, class Cfg>
-int run_gate_up(const void* x, int top_k, const int32_t* perm, const int32_t* offsets, int n_local,
-                int64_t max_rows, const void* w_in, int hidden, int inter, void* act,
+int run_gate_up(const void* x, int64_t n_tokens, int top_k, const int32_t* perm, const int32_t* offsets,
+                int n_local, int64_t max_rows, const void* w_in, int hidden, int inter, void* act,
                 hipStream_t stream) {
   GemmParams g1;
   g1.A = x; g1.perm = perm; g1.offsets = offsets; g1.W = w_in; g1.C = act;
   g1.w_expert_stride = static_cast<int64_t>(2) * inter * hidden;
   g1.n_local = n_local; g1.top_k = top_k; g1.K = hidden; g1.N = inter;
   g1.n_tiles_n = inter / (Cfg::BN / 2);
-  hipError_t e = launch<DT, Cfg, true>(g1, max_rows, stream);
+  g1.a_bytes = static_cast<uint32_t>(n_tokens * hidden * dtype_bytes(DT));
+  div_magic(static_cast<uint32_t>(top_k), &g1.k_magic, &g1.k_shift);
+  hipError_t e;
+  if (DT == MEP_DTYPE_BF16 && hidden >= 8 * bfk::KS) e = launch_bf16<true>(g1, max_rows, stream);
+  else e = launch<DT, Cfg, true>(g1, max_rows, stream);
   MEP_REQUIRE(e == hipSuccess, MEP_ERR_HIP, "mep_swiglu_gate_up: %s", hipGetErrorString(e));
   return MEP_OK;
 }
@@ -413,7 +820,11 @@ int run_down(const void* act, int top_k, const int32_t* perm, const int32_t* off
   g2.w_expert_stride = static_cast<int64_t>(hidden) * inter;
   g2.n_local = n_local; g2.top_k = top_k; g2.K = inter; g2.N = hidden;
   g2.n_tiles_n = hidden / Cfg::BN;
-  hipError_t e = launch<DT, Cfg, false>(g2, max_rows, stream);
+  g2.a_bytes = static_cast<uint32_t>(max_rows * inter * dtype_bytes(DT));
+  div_magic(static_cast<uint32_t>(top_k), &g2.k_magic, &g2.k_shift);
+  hipError_t e;
+  if (DT == MEP_DTYPE_BF16 && inter >= 8 * bfk::KS) e = launch_bf16<false>(g2, max_rows, stream);
+  else e = launch<DT, Cfg, false>(g2, max_rows, stream);
   MEP_REQUIRE(e == hipSuccess, MEP_ERR_HIP, "mep_swiglu_down: %s", hipGetErrorString(e));
   return MEP_OK;
 }
@@ -463,9 +874,9 @@ extern "C" int mep_swiglu_gate_up(const void* x, int64_t n_tokens, int32_t top_k
               "mep_swiglu_gate_up: buffers must be 16-byte aligned");
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == MEP_DTYPE_BF16)
-    return run_gate_up<MEP_DTYPE_BF16, CfgBf16>(x, top_k, perm, offsets, n_local, max_rows, w_in, hidden,
-                                                inter, act, s);
-  return run_gate_up<MEP_DTYPE_F32, CfgF32>(x, top_k, perm, offsets, n_local, max_rows, w_in, hidden,
+    return run_gate_up<MEP_DTYPE_BF16, CfgBf16>(x, n_tokens, top_k, perm, offsets, n_local, max_rows, w_in,
+                                                hidden, inter, act, s);
+  return run_gate_up<MEP_DTYPE_F32, CfgF32>(x, n_tokens, top_k, perm, offsets, n_local, max_rows, w_in, hidden,
                                             inter, act, s);
 }
 
