@@ -403,56 +403,57 @@ hipError_t launch(const GemmParams& p, int64_t max_rows, hipStream_t stream) {
 }
 
 // ============================================================================
-// bf16 path: 8 waves, 4-stage LDS ring, AGPR accumulators.
+// bf16 path: 8 waves, two 64 KiB LDS stages of two K-steps each, AGPR
+// accumulators.
 //
 // Tile 256 x 256 (GEMM-1: 128 gate + 128 up columns), 8 waves (4 x 2) of
-// 64 x 128.  K moves 32 bf16 (64 B per row) per step through a ring of four
-// 32 KiB LDS stages filled by global_load_lds_dwordx4 three steps ahead of the
-// MFMAs that consume them; the ring runs on across tile boundaries, so the
-// next tile's first three steps stream in while this tile's last steps and its
-// epilogue run.  During step s each wave
-//   - issues its 4 DMA blocks of step s+3 (one per group of 8 MFMAs),
-//   - reads the fragments of step s+1 (3 ds_read_b128 per group) into the
-//     other register set,
-//   - runs the 32 MFMAs of step s on the fragments read during step s-1,
-// then waits for step s+2's DMA (vmcnt) and joins an LDS-only barrier.
-// The MFMAs are inline asm with "+a" accumulators: the compiler keeps the
-// 128 accumulators in AGPRs and does not shuffle them between register
-// files (with the builtin it does, and spills).  Measured on the K loop alone
-// (streamed A rows): this schedule beats the two-stage 128 B/row loop by
-// about 15 %.
+// 64 x 128.  One MFMA step covers 32 of K; a stage holds two steps (128 bytes
+// of every A row and weight row) and is filled by buffer_load_dwordx4 ... lds:
+// one instruction moves 8 whole 128-byte lines (full lines move about 25 %
+// faster than the 64-byte half lines of one-step stages; measured).  Stage d
+// of a tile sits in buffer d & 1, and the stages of consecutive tiles run on
+// through the same two buffers, so the next tile's first stages stream in
+// while this tile's last steps and its epilogue run.  Within stage d:
+//   even step 2d   - MFMAs on the fragments of step 2d (read during step 2d-1),
+//                    read the fragments of step 2d+1 (same stage), then wait
+//                    for stage d+1's DMA and join a barrier;
+//   odd step 2d+1  - issue stage d+2's DMA into buffer d & 1 (free: its last
+//                    fragments were read during step 2d, before that barrier),
+//                    MFMAs on step 2d+1, read the fragments of step 2d+2 from
+//                    stage d+1 (published by that barrier).  No barrier.
+// So a stage's DMA has two steps to land, and there is one barrier per stage.
+// MFMAs run column-major (the 4 MFMAs of weight fragment j, then j+1): row
+// fragments are double-buffered, weight fragment j is refilled right after its
+// group.  The MFMAs are inline asm with "+a" accumulators, which keeps the 128
+// accumulators in AGPRs (with the builtin the compiler moves them between
+// register files and spills).
 //
-// Epilogue: stage s_last % 4 is free between the last step of a tile and the
-// next step (its fragments were read during step s_last - 1 and the next DMA
-// into it is issued at step s_last + 1), so the output is staged through it in
-// passes of 64 columns x 256 rows (128-byte rows XOR-swizzled by r & 7) and
-// stored with 16-byte coalesced stores.  The K order of a tile is rotated by
-// its column-tile index (n_tile * KT / 4 steps), which spreads the tiles that
-// run at the same time over more HBM / L2 channels; the rotation depends on
-// the output columns only, so every output element is summed in the same
-// order wherever its row sits in the dispatch.
+// Epilogue straight from the accumulators (16-byte stores, see pair_cols), no
+// LDS and no barrier.  The K order of a tile is rotated by its column-tile
+// index (n_tile * KD / 4 stages), which spreads the tiles running at the same
+// time over more memory channels; the rotation depends only on the output
+// columns, so every output element is summed in the same order wherever its
+// row sits in the dispatch.
 namespace bfk {
 constexpr int BM = 256, BN = 256, NT = 512, NW = 8;
-constexpr int RB = 64;                        // bytes per row per step
-constexpr int KS = RB / 2;                    // bf16 elements per step
-constexpr int STEP = (BM + BN) * RB;          // 32 KiB per stage
-constexpr int NSTAGE = 4;
-constexpr int ASTAGE = BM * RB;                    // A rows of one stage (16 KiB); the weight rows take as much
-static_assert(BN * RB == ASTAGE, "A and weight rows of a stage are the same size");
-constexpr int BREGION = NSTAGE * ASTAGE;           // weight rows of all stages start here (64 KiB)
+constexpr int KS = 32;                        // K per MFMA step (16x16x32)
+constexpr int RB = 128;                       // bytes per row of a stage: two steps of K
+constexpr int HALF = BM * RB;                 // A rows of one stage (32 KiB); the weight rows take as much
+constexpr int BREGION = 2 * HALF;             // weight rows of both stages start at 64 KiB
 constexpr int MF = 4, NF = 8;                 // 16 x 16 fragments per wave (64 x 128)
-constexpr int BPW = 4;                        // 1 KiB DMA blocks (16 rows x 64 B) per wave per step
+constexpr int BPW = 8;                        // 1 KiB DMA blocks (8 rows x 128 B) per wave per stage
 constexpr int NLMAX = 256;
-constexpr int LDS_BYTES = NSTAGE * STEP + (2 * (NLMAX + 1) + 2 * BM) * 4;
+constexpr int LDS_BYTES = 4 * HALF + (2 * (NLMAX + 1) + 2 * BM) * 4;
 // buffer resource word 3 for raw 32-bit buffer access on gfx9-family parts
 constexpr int kBufWord3 = 0x00020000;
-static_assert(BPW == MF, "one DMA block per MFMA group");
-static_assert((BM + BN) / 16 == NW * BPW, "DMA blocks cover the stage");
+static_assert(BN * RB == HALF, "A and weight rows of a stage are the same size");
+static_assert((BM + BN) / 8 == NW * BPW, "DMA blocks cover the stage");
+static_assert(BPW == NF, "one DMA block per MFMA group of an odd step");
 }  // namespace bfk
 
 // 16x16x32 bf16 MFMA with the accumulator pinned to AGPRs; src0 = weight
 // fragment, src1 = row fragment, so the result is C^T (lane: one row, 4
-// consecutive columns).  ZERO starts a new accumulation (C operand 0).
+// consecutive columns).  mfma_first starts a new accumulation (C operand 0).
 __device__ __forceinline__ void mfma_acc(f32x4& acc, const u32x4& w, const u32x4& a) {
   asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(w), "v"(a));
 }
@@ -467,18 +468,28 @@ __device__ __forceinline__ void pin_acc(f32x4& acc) { asm volatile("" : "+a"(acc
 // base + voff + soff land at lds + 16 L; an offset at or past `bytes` reads
 // zeros instead of faulting.  (A plain device function: inside the kernel
 // template the host pass drops the kernel's launch stub.)
+// The resource is rebuilt from scalars read with readfirstlane: wherever the
+// compiler kept base / bytes, the descriptor is then in SGPRs (a descriptor it
+// thinks may be divergent gets a readfirstlane loop around every load).
 __device__ __forceinline__ void buffer_lds_16(const unsigned char* base, int bytes, uint32_t voff, int soff,
                                               unsigned char* lds) {
+  // readfirstlane returns int: cast each half to uint32_t before widening, or
+  // a low word with bit 31 set would sign-extend over the high word
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(b >> 32)));
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(b & 0xFFFFFFFFu)));
+  const uint64_t bs = (static_cast<uint64_t>(hi) << 32) | lo;
   __builtin_amdgcn_raw_ptr_buffer_load_lds(
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(base), 0, bytes, bfk::kBufWord3),
-      (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
+      __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(bs), 0, __builtin_amdgcn_readfirstlane(bytes),
+                                        bfk::kBufWord3),
+      (__attribute__((address_space(3))) void*)lds, 16, voff, __builtin_amdgcn_readfirstlane(soff), 0, 0);
 }
 
 template <bool GEMM1>
 __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
   using namespace bfk;
   __shared__ __attribute__((aligned(16))) unsigned char smem[LDS_BYTES];
-  int* const s_prefix = reinterpret_cast<int*>(smem + NSTAGE * STEP);   // [NLMAX + 1] tiles before expert j
+  int* const s_prefix = reinterpret_cast<int*>(smem + 4 * HALF);       // [NLMAX + 1] tiles before expert j
   int* const s_off = s_prefix + NLMAX + 1;                             // [NLMAX + 1] row offsets
   int* const s_rows = s_off + NLMAX + 1;                               // [2][BM] row maps
 
@@ -488,7 +499,8 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
   const int K = p.K;
-  const int KT = K / KS;                      // steps per tile (even, >= 4, multiple of 4)
+  const int KD = K / (2 * KS);                // stages per tile (a multiple of 4, >= 4)
+  const int KT = 2 * KD;                      // MFMA steps per tile
   const int nl = p.n_local;
 
   // ---- tile table ---------------------------------------------------------------
@@ -502,28 +514,61 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
     for (int j = 0; j < nl; ++j) s_prefix[j + 1] += s_prefix[j];
   __syncthreads();
   const int total = __builtin_amdgcn_readfirstlane(s_prefix[nl]);
+  // Work items.  XCD x owns tiles [x_lo, x_hi); its nslots workgroups take
+  // items slot, slot + nslots, ...  When the XCD's tile count leaves a
+  // remainder L <= nslots / 2 after whole rounds, its first L tiles are split
+  // into 2 L row halves (128 rows each) that come first, one per workgroup, so
+  // the last round does not leave most workgroups idle.  A row half sums every
+  // output element in the same order as the whole tile.
   const int per_xcd = (total + 7) / 8;
   const int xcd = blockIdx.x % 8, slot = blockIdx.x / 8, nslots = gridDim.x / 8;
-  const int n_my = slot < per_xcd ? (per_xcd - slot + nslots - 1) / nslots : 0;
-  auto tile_id = [&](int i) { return xcd * per_xcd + slot + i * nslots; };
-  auto tile_valid = [&](int i) { return i < n_my && tile_id(i) < total; };
+  const int x_lo = min(total, xcd * per_xcd), x_hi = min(total, x_lo + per_xcd);
+  const int rem = (x_hi - x_lo) % nslots;
+  const int n_half = (2 * rem <= nslots) ? 2 * rem : 0;
+  const int n_items = x_hi - x_lo + n_half / 2;
+  const int n_my = slot < n_items ? (n_items - slot + nslots - 1) / nslots : 0;
+  auto tile_valid = [&](int i) { return i < n_my; };
   if (!tile_valid(0)) return;
 
-  struct Tile { int e, row0, row_end, nt; };
-  auto decode = [&](int lt) {
-    int lo = 0, hi = nl - 1;
+  // row0 .. row0+255: the rows a tile computes (loads clamp to row_end - 1);
+  // rows at or past valid_end are not stored; waves with wm >= act_wm compute
+  // nothing (a row half runs on the 4 waves of rows 0..127, one per SIMD).
+  struct Tile { int e, row0, row_end, valid_end, nt, act_wm; };
+  auto decode_tile = [&](int lt) {
+    int lo = 0, hi = nl - 1;                       // largest j with s_prefix[j] <= lt
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
       if (s_prefix[mid] <= lt) lo = mid; else hi = mid - 1;
     }
     const int u = lt - s_prefix[lo];
-    Tile t;
+    Tile t;                                        // uniform: keep it in SGPRs
     t.e = __builtin_amdgcn_readfirstlane(lo);
     t.row0 = __builtin_amdgcn_readfirstlane(s_off[lo] + (u / p.n_tiles_n) * BM);
     t.row_end = __builtin_amdgcn_readfirstlane(s_off[lo + 1]);
     t.nt = __builtin_amdgcn_readfirstlane(u % p.n_tiles_n);
+    t.valid_end = t.row_end;
+    t.act_wm = 4;
     return t;
   };
+  auto decode = [&](int i) {
+    const int u = slot + i * nslots;
+    if (u >= n_half) return decode_tile(x_lo + n_half / 2 + (u - n_half));
+    Tile t = decode_tile(x_lo + u / 2);
+    const int r0 = t.row0 + (u & 1) * (BM / 2);
+    if (r0 < t.row_end) {
+      t.row0 = r0;
+      t.valid_end = min(t.row_end, r0 + BM / 2);
+      t.act_wm = 2;
+    } else {                                   // empty half: addresses of the tile, nothing computed
+      t.valid_end = t.row0;
+      t.act_wm = 0;
+    }
+    return t;
+  };
+  // row map: perm[row0 .. row0 + BM) of a tile DMA'd into LDS (clamped to the
+  // tile's last row, so every lane reads inside perm).  GEMM-1 gathers its A
+  // rows through it, GEMM-2 scatters its output rows.
+  static_assert(BM % 64 == 0 && BM / 64 <= NW, "row-map DMA: one 64-row instruction per wave");
   auto rowmap_dma = [&](const Tile& t, int parity) {
     if (wave < BM / 64) {
       const int r = min(t.row0 + wave * 64 + lane, t.row_end - 1);
@@ -534,11 +579,11 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
   };
 
   // ---- DMA sources ----------------------------------------------------------------
-  // Block q = wave * BPW + i holds stage rows 16q .. 16q+15 (A rows 0..255, then
-  // weight rows); lane L moves 16 B of row 16q + L/4 into byte 16 L of the
-  // block, i.e. physical chunk L & 3, and fetches logical chunk
-  // (L & 3) ^ ((row >> 1) & 3): 64-byte rows XOR-swizzled by (r >> 1) & 3,
-  // which makes the fragment reads conflict-free.
+  // Block q = wave * BPW + i (waves 0-3: A rows 8q .. 8q+7; waves 4-7: weight
+  // rows 8(q - 32) ..); lane L moves 16 B of row 8q + L/8 into byte 16 L of
+  // the block, i.e. physical chunk L & 7, and fetches logical chunk
+  // (L & 7) ^ (row & 7): 128-byte rows XOR-swizzled by r & 7, which makes the
+  // fragment reads conflict-free.
   const bool wave_a = wave < 4;
   // Output columns of a weight stage row.  Within each aligned group of 32
   // rows (two 16-column fragments j, j+1), fragment row n of fragment j2 holds
@@ -550,100 +595,131 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
   // __amdgpu_buffer_rsrc_t makes the host pass drop the kernel's launch stub
   struct Src { const unsigned char* base; int bytes; uint32_t off[BPW]; int rot; };
   auto setup = [&](const Tile& t, int parity) {
-    int lrow = lane >> 2, lchunk = (lane & 3) ^ ((lane >> 3) & 3);
+    // recompute the per-lane row terms here instead of keeping them live across
+    // the whole tile loop (hoisted, they outgrow the register budget and spill)
+    int lrow = lane >> 3, lchunk = (lane & 7) ^ (lane >> 3);
     asm volatile("" : "+v"(lrow), "+v"(lchunk));
+    int wv = wave;                             // opaque here too: no per-block constant is hoisted
+    asm volatile("" : "+s"(wv));
     Src s;
-    s.rot = (KT % 4 == 0) ? (t.nt * (KT / 4)) % KT : 0;
+    s.rot = (KD % 4 == 0) ? (t.nt & 3) * (KD / 4) : 0;
     if (wave_a) {
       s.base = static_cast<const unsigned char*>(p.A);
       s.bytes = static_cast<int>(p.a_bytes);
+      // 32-bit offsets: the size checks keep A below 4 GiB
+      const uint32_t lane_off = static_cast<uint32_t>(lchunk * 16);
 #pragma unroll
       for (int i = 0; i < BPW; ++i) {
-        const int r = (wave * BPW + i) * 16 + lrow;
-        int64_t src_row;
+        const int r0 = (wv * BPW + i) * 8;                  // wave-uniform
+        uint32_t src_row;
         if constexpr (GEMM1) {
-          const uint32_t f = static_cast<uint32_t>(s_rows[parity * BM + r]);   // flat entry t*k + s
+          const uint32_t f = static_cast<uint32_t>(s_rows[parity * BM + r0 + lrow]);   // flat entry t*k + s
           src_row = p.k_magic ? (__umulhi(f, p.k_magic) >> p.k_shift) : f;
+        } else {
+          src_row = static_cast<uint32_t>(min(t.row0 + r0 + lrow, t.row_end - 1));
         }
-        else src_row = min(t.row0 + r, t.row_end - 1);
-        s.off[i] = static_cast<uint32_t>((src_row * K + lchunk * 8) * 2);
+        s.off[i] = src_row * static_cast<uint32_t>(K * 2) + lane_off;
       }
     } else {
       s.base = static_cast<const unsigned char*>(p.W) + static_cast<int64_t>(t.e) * p.w_expert_stride * 2;
       s.bytes = static_cast<int>(p.w_expert_stride * 2);
+      // weight row of stage row rb0 + lrow (rb0 = the block's first row, a
+      // multiple of 8): pair_cols(rb0) + lane part, so the row split into a
+      // scalar per block and one per-lane term
+      const int lp = ((lrow & 4) << 1) | (lrow & 3);
+      const uint32_t lane_off = static_cast<uint32_t>((lp * K + lchunk * 8) * 2);
 #pragma unroll
       for (int i = 0; i < BPW; ++i) {
-        const int rb = (wave * BPW + i) * 16 + lrow - BM;
-        int wrow;
-        if constexpr (GEMM1) wrow = (rb < BN / 2) ? t.nt * (BN / 2) + pair_cols(rb) : p.N + t.nt * (BN / 2) + pair_cols(rb - BN / 2);
-        else wrow = t.nt * BN + pair_cols(rb);
-        s.off[i] = static_cast<uint32_t>((static_cast<int64_t>(wrow) * K + lchunk * 8) * 2);
+        const int rb0 = ((wv - 4) * BPW + i) * 8;          // wave-uniform
+        int wrow0;
+        if constexpr (GEMM1) wrow0 = (rb0 < BN / 2) ? t.nt * (BN / 2) + pair_cols(rb0) : p.N + t.nt * (BN / 2) + pair_cols(rb0 - BN / 2);
+        else wrow0 = t.nt * BN + pair_cols(rb0);
+        s.off[i] = static_cast<uint32_t>(wrow0 * K * 2) + lane_off;
       }
     }
     return s;
   };
-  // per-lane 32-bit offset, the K position in the scalar offset
-  // LDS layout: the A rows of stage s at s * 16 KiB, its weight rows at
-  // 64 KiB + s * 16 KiB, so every fragment read of the ring is one of two
-  // base registers plus an immediate below 64 KiB
+  // stage buffers: A rows of buffer b at b * 32 KiB, weight rows at
+  // 64 KiB + b * 32 KiB, so each fragment read is one of four base registers
+  // plus an immediate below 64 KiB
   const int lds_blk = wave_a ? wave * BPW * 1024 : BREGION + (wave - 4) * BPW * 1024;
-  auto dma_blk = [&](const Src& s, int kt, int stage, int i) {
-    int kd = kt + s.rot;
-    if (kd >= KT) kd -= KT;
-    buffer_lds_16(s.base, s.bytes, s.off[i], kd * RB, smem + lds_blk + stage * ASTAGE + i * 1024);
+  auto dma_blk = [&](const Src& s, int kd, int buf, int i) {
+    int ke = kd + s.rot;
+    if (ke >= KD) ke -= KD;
+    // opaque: otherwise the 16 destinations (buffer x block) are hoisted into
+    // scalar registers, which the loop does not have to spare
+    int lb = lds_blk;
+    asm volatile("" : "+s"(lb));
+    buffer_lds_16(s.base, s.bytes, s.off[i], ke * RB, smem + lb + buf * HALF + i * 1024);
   };
 
   // ---- fragments ------------------------------------------------------------------
+  // Lane (lr, lg) reads 16 B of row 16 i + lr at logical chunk 4 kk + lg
+  // (kk = step parity within the stage), stored at chunk (4 kk + lg) ^ (lr & 7).
   const int lr = lane & 15, lg = lane >> 4;
-  const uint32_t cpo = static_cast<uint32_t>((lg ^ ((lr >> 1) & 3)) << 4);
-  const uint32_t a_lane = static_cast<uint32_t>((wm * 64 + lr) * RB) + cpo;
-  uint32_t b_lo, b_hi;   // GEMM-1: gate / up fragment rows; GEMM-2: one contiguous range
-  if constexpr (GEMM1) {
-    b_lo = static_cast<uint32_t>(BREGION + (wn * 64 + lr) * RB) + cpo;
-    b_hi = static_cast<uint32_t>(BREGION + (BN / 2 + wn * 64 + lr) * RB) + cpo;
-  } else {
-    b_lo = static_cast<uint32_t>(BREGION + (wn * 128 + lr) * RB) + cpo;
-    b_hi = b_lo + 4 * 16 * RB;
+  uint32_t a_base[2], b_base[2];
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk) {
+    const uint32_t cp = static_cast<uint32_t>(((4 * kk + lg) ^ (lr & 7)) << 4);
+    a_base[kk] = static_cast<uint32_t>((wm * 64 + lr) * RB) + cp;
+    if constexpr (GEMM1) b_base[kk] = static_cast<uint32_t>(BREGION + (wn * 64 + lr) * RB) + cp;
+    else b_base[kk] = static_cast<uint32_t>(BREGION + (wn * 128 + lr) * RB) + cp;
   }
-  auto b_addr = [&](int j) { return (j < 4 ? b_lo + j * 16 * RB : b_hi + (j - 4) * 16 * RB); };
-  // Row fragments are double-buffered (fa[set]); weight fragments are not: the
-  // MFMAs run column-major (group j = the 4 MFMAs that use weight fragment j),
-  // so fb[j] is refilled with the next step's fragment right after group j.
-  // (An MFMA reads its A/B operands when it issues.)  64 fragment VGPRs.
+  // weight fragment j: GEMM-1 gate rows j < 4, up rows (128 rows further) j >= 4
+  auto b_off = [&](int j) { return GEMM1 ? (j < 4 ? j * 16 * RB : (BN / 2 + (j - 4) * 16) * RB) : j * 16 * RB; };
   u32x4 fa[2][MF], fb[NF];
   f32x4 acc[MF][NF];
 
-  // One step: MFMAs on fa[SET] / fb (read during the previous step); with DMA,
-  // issue the 4 blocks of step dkt of the tile `s` describes into stage
-  // dstage (one every other group); with RD, read the next step's fragments
-  // from stage rstage.  ZERO starts the accumulation.
-  auto step = [&](auto set_c, auto zero_c, auto dma_c, auto rd_c, const Src& s, int dkt, int dstage, int rstage) {
+  // One step: MFMAs on fa[SET] / fb.  EVEN steps read the fragments of the
+  // step's second half of the stage in buffer rbuf and end with the stage
+  // wait + barrier; ODD steps issue the DMA of stage dkd (of the tile `s`
+  // describes) into buffer dbuf, one block per MFMA group, and read the next
+  // stage's first-step fragments from rbuf (unless !RD).  ZERO starts the
+  // accumulation.  An idle wave of a row-half tile only moves its DMA blocks.
+  auto step = [&](auto set_c, auto zero_c, auto odd_c, auto rd_c, const Src& s, int dkd, int dbuf, int rbuf,
+                  bool act) {
     constexpr int SET = decltype(set_c)::value;
-    constexpr bool ZERO = decltype(zero_c)::value, DMA = decltype(dma_c)::value, RD = decltype(rd_c)::value;
-    const unsigned char* R = smem + rstage * ASTAGE;
+    constexpr bool ZERO = decltype(zero_c)::value, ODD = decltype(odd_c)::value, RD = decltype(rd_c)::value;
+    constexpr int RKK = ODD ? 0 : 1;                 // which half of the stage the read fragments are
+    const unsigned char* R = smem + rbuf * HALF;
+    if (!act) {
+      if constexpr (ODD) {
 #pragma unroll
-    for (int j = 0; j < NF; ++j) {
-      if constexpr (DMA) {
-        if (j % 2 == 0) dma_blk(s, dkt, dstage, j / 2);
+        for (int i = 0; i < BPW; ++i) dma_blk(s, dkd, dbuf, i);
       }
+    } else {
 #pragma unroll
-      for (int i = 0; i < MF; ++i) {
-        if constexpr (ZERO) mfma_first(acc[i][j], fb[j], fa[SET][i]);
-        else mfma_acc(acc[i][j], fb[j], fa[SET][i]);
+      for (int j = 0; j < NF; ++j) {
+        if constexpr (ODD) dma_blk(s, dkd, dbuf, j);
+#pragma unroll
+        for (int i = 0; i < MF; ++i) {
+          if constexpr (ZERO) mfma_first(acc[i][j], fb[j], fa[SET][i]);
+          else mfma_acc(acc[i][j], fb[j], fa[SET][i]);
+        }
+        if constexpr (RD) {
+          fb[j] = *reinterpret_cast<const u32x4*>(R + b_base[RKK] + b_off(j));
+          if (j % 2 == 1)
+            fa[SET ^ 1][j / 2] = *reinterpret_cast<const u32x4*>(R + a_base[RKK] + (j / 2) * 16 * RB);
+        }
+        asm volatile("" ::: "memory");
       }
-      if constexpr (RD) {
-        fb[j] = *reinterpret_cast<const u32x4*>(R + b_addr(j));
-        if (j % 2 == 1) fa[SET ^ 1][j / 2] = *reinterpret_cast<const u32x4*>(R + a_lane + (j / 2) * 16 * RB);
-      }
-      asm volatile("" ::: "memory");
     }
-    // publish: the DMA of step (this step + 2) has landed, every read of this
-    // step is done.  vmcnt(BPW) suffices whatever else is outstanding (the
-    // previous epilogue's stores): loads complete in order, and this step's
-    // BPW DMA blocks were issued after step+2's.
-    if constexpr (DMA) __builtin_amdgcn_s_waitcnt(0x0F70 | BPW);
-    else __builtin_amdgcn_s_waitcnt(kVmcnt0);
-    lds_barrier();
+    if constexpr (!ODD) {
+      // the stage DMA'd during the previous step has landed (nothing else this
+      // wave issued since is a load), every fragment read of this step is done
+      __builtin_amdgcn_s_waitcnt(kVmcnt0);
+      lds_barrier();
+    }
+  };
+  // fragments of a tile's first step (stage 0 = buffer 0, first half): read at
+  // the tile start, after the previous epilogue, so no fragment registers are
+  // live across an epilogue
+  auto first_frags = [&]() {
+#pragma unroll
+    for (int g = 0; g < MF; ++g) fa[0][g] = *reinterpret_cast<const u32x4*>(smem + a_base[0] + g * 16 * RB);
+#pragma unroll
+    for (int j = 0; j < NF; ++j) fb[j] = *reinterpret_cast<const u32x4*>(smem + b_base[0] + b_off(j));
+    __builtin_amdgcn_s_waitcnt(kLgkmcnt0);
   };
 
   // ---- epilogue -----------------------------------------------------------------------
@@ -657,6 +733,7 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
   T* const C = static_cast<T*>(p.C);
   constexpr int CN = GEMM1 ? BN / 2 : BN;     // output columns per tile
   auto epilogue = [&](const Tile& t, int parity) {
+    if (wm >= t.act_wm) return;
     // the last MFMAs' results must be written before the AGPRs are read (the
     // asm hides the MFMAs from the hazard recognizer): pad, then tie every
     // accumulator to an (empty) asm after the padding so no read moves above it
@@ -678,7 +755,7 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
       if constexpr (GEMM1) row = t.row0 + r;
       else row = s_rows[parity * BM + r];                                   // (token, slot) cell
       T* const dst = C + row * p.N + col;
-      const bool ok = t.row0 + r < t.row_end;
+      const bool ok = t.row0 + r < t.valid_end;
 #pragma unroll
       for (int jp = 0; jp < (GEMM1 ? NF / 4 : NF / 2); ++jp) {             // fragment pairs (2 jp, 2 jp + 1)
         float v[8];
@@ -698,67 +775,54 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
   };
 
   // ---- persistent step loop ---------------------------------------------------------
-  // Invariant at the start of step kt of a tile: stages kt%4 and (kt+1)%4 hold
-  // their data (waited + barrier), the fragments of step kt are in register set
-  // kt&1, the DMA of step kt+2 is in flight.  Steps of consecutive tiles share
-  // the ring; KT % 4 == 0, so step kt of every tile uses stage kt % 4.
-  Tile cur = decode(tile_id(0));
+  Tile cur = decode(0);
   bool has_next = tile_valid(1);
-  Tile nxt = has_next ? decode(tile_id(1)) : cur;
+  Tile nxt = has_next ? decode(1) : cur;
   rowmap_dma(cur, 0);
   if (has_next) rowmap_dma(nxt, 1);
   __builtin_amdgcn_s_waitcnt(kVmcnt0);
   lds_barrier();
   Src sc = setup(cur, 0);
 #pragma unroll
-  for (int g = 0; g < BPW; ++g) dma_blk(sc, 0, 0, g);
+  for (int i = 0; i < BPW; ++i) dma_blk(sc, 0, 0, i);
 #pragma unroll
-  for (int g = 0; g < BPW; ++g) dma_blk(sc, 1, 1, g);
+  for (int i = 0; i < BPW; ++i) dma_blk(sc, 1, 1, i);
   __builtin_amdgcn_s_waitcnt(kVmcnt0);
   lds_barrier();
-#pragma unroll
-  for (int g = 0; g < BPW; ++g) dma_blk(sc, 2, 2, g);
-  // fragments of a tile's step 0 (stage 0): read at the tile start, after the
-  // previous epilogue, so no fragment registers are live across an epilogue
-  auto first_frags = [&]() {
-#pragma unroll
-    for (int g = 0; g < MF; ++g) fa[0][g] = *reinterpret_cast<const u32x4*>(smem + a_lane + g * 16 * RB);
-#pragma unroll
-    for (int j = 0; j < NF; ++j) fb[j] = *reinterpret_cast<const u32x4*>(smem + b_addr(j));
-    __builtin_amdgcn_s_waitcnt(kLgkmcnt0);
-  };
 
   std::integral_constant<int, 0> S0;
   std::integral_constant<int, 1> S1;
   std::integral_constant<bool, false> NO;
   std::integral_constant<bool, true> YES;
+  // Invariant at a tile's start: its stages 0 and 1 are in buffers 0 and 1
+  // (landed, published).  Steps are unrolled by four (two stages), so every
+  // buffer index is an immediate.
   for (int it = 0;; ++it) {
-    first_frags();
-    // steps are unrolled by four so every stage offset is an immediate: step
-    // kt reads stage (kt+1)&3 and DMAs into stage (kt+3)&3
-    step(S0, YES, YES, YES, sc, 3, 3, 1);
+    const bool act = wm < cur.act_wm;
+    if (act) first_frags();
+    step(S0, YES, NO, YES, sc, 0, 0, 0, act);          // step 0 (stage 0)
     // every wave is past its previous epilogue (barrier above), so the row
-    // map buffer that epilogue read can take the next tile's row map; it
-    // lands by the end of step 1 and is read by setup() at step KT-3
+    // map buffer that epilogue read can take the next tile's row map; the
+    // wait at the end of step 2 covers it, setup() reads it at step KT-3
     if (it > 0 && has_next) rowmap_dma(nxt, (it + 1) & 1);
-    step(S1, NO, YES, YES, sc, 4, 0, 2);
-    step(S0, NO, YES, YES, sc, 5, 1, 3);
-    step(S1, NO, YES, YES, sc, 6, 2, 0);
-    // steady state: steps 4m .. 4m+3 DMA steps 4m+3 .. 4m+6 of this tile
+    step(S1, NO, YES, YES, sc, 2, 0, 1, act);          // step 1: DMA stage 2 -> buffer 0
+    step(S0, NO, NO, YES, sc, 0, 0, 1, act);           // step 2 (stage 1)
+    step(S1, NO, YES, YES, sc, 3, 1, 0, act);          // step 3: DMA stage 3 -> buffer 1
+    // steady state: steps k4 .. k4+3 (stages k4/2, k4/2 + 1) DMA stages k4/2 + 2, + 3
     for (int k4 = 4; k4 < KT - 4; k4 += 4) {
-      step(S0, NO, YES, YES, sc, k4 + 3, 3, 1);
-      step(S1, NO, YES, YES, sc, k4 + 4, 0, 2);
-      step(S0, NO, YES, YES, sc, k4 + 5, 1, 3);
-      step(S1, NO, YES, YES, sc, k4 + 6, 2, 0);
+      step(S0, NO, NO, YES, sc, 0, 0, 0, act);
+      step(S1, NO, YES, YES, sc, k4 / 2 + 2, 0, 1, act);
+      step(S0, NO, NO, YES, sc, 0, 0, 1, act);
+      step(S1, NO, YES, YES, sc, k4 / 2 + 3, 1, 0, act);
     }
-    // last four steps: KT-4 DMAs this tile's last step, the other three the
-    // next tile's steps 0..2.  Without a next tile they re-read this tile's
-    // steps 0..2 (in bounds, never consumed) so the code has no branch here.
-    step(S0, NO, YES, YES, sc, KT - 1, 3, 1);
-    sc = has_next ? setup(nxt, (it + 1) & 1) : setup(cur, it & 1);   // next row map landed during step 0
-    step(S1, NO, YES, YES, sc, 0, 0, 2);
-    step(S0, NO, YES, YES, sc, 1, 1, 3);
-    step(S1, NO, YES, NO, sc, 2, 2, 0);
+    // last two stages: their odd steps DMA the next tile's stages 0 and 1.
+    // Without a next tile they re-read this tile's (in bounds, never consumed)
+    // so the code has no branch here.
+    step(S0, NO, NO, YES, sc, 0, 0, 0, act);           // step KT-4
+    sc = has_next ? setup(nxt, (it + 1) & 1) : setup(cur, it & 1);
+    step(S1, NO, YES, YES, sc, 0, 0, 1, act);          // step KT-3: next stage 0 -> buffer 0
+    step(S0, NO, NO, YES, sc, 0, 0, 1, act);           // step KT-2
+    step(S1, NO, YES, NO, sc, 1, 1, 0, act);           // step KT-1: next stage 1 -> buffer 1
     epilogue(cur, it & 1);
     if (!has_next) {
       // no DMA may still be writing this workgroup's LDS when its waves end
@@ -767,7 +831,7 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
     }
     cur = nxt;
     has_next = tile_valid(it + 2);
-    if (has_next) nxt = decode(tile_id(it + 2));
+    if (has_next) nxt = decode(it + 2);
   }
 }
 
@@ -806,7 +870,7 @@ int run_gate_up(const void* x, int64_t n_tokens, int top_k, const int32_t* perm,
   g1.a_bytes = static_cast<uint32_t>(n_tokens * hidden * dtype_bytes(DT));
   div_magic(static_cast<uint32_t>(top_k), &g1.k_magic, &g1.k_shift);
   hipError_t e;
-  if (DT == MEP_DTYPE_BF16 && hidden >= 8 * bfk::KS) e = launch_bf16<true>(g1, max_rows, stream);
+  if (DT == MEP_DTYPE_BF16 && hidden % 256 == 0) e = launch_bf16<true>(g1, max_rows, stream);
   else e = launch<DT, Cfg, true>(g1, max_rows, stream);
   MEP_REQUIRE(e == hipSuccess, MEP_ERR_HIP, "mep_swiglu_gate_up: %s", hipGetErrorString(e));
   return MEP_OK;
@@ -823,7 +887,7 @@ int run_down(const void* act, int top_k, const int32_t* perm, const int32_t* off
   g2.a_bytes = static_cast<uint32_t>(max_rows * inter * dtype_bytes(DT));
   div_magic(static_cast<uint32_t>(top_k), &g2.k_magic, &g2.k_shift);
   hipError_t e;
-  if (DT == MEP_DTYPE_BF16 && inter >= 8 * bfk::KS) e = launch_bf16<false>(g2, max_rows, stream);
+  if (DT == MEP_DTYPE_BF16 && inter % 256 == 0) e = launch_bf16<false>(g2, max_rows, stream);
   else e = launch<DT, Cfg, false>(g2, max_rows, stream);
   MEP_REQUIRE(e == hipSuccess, MEP_ERR_HIP, "mep_swiglu_down: %s", hipGetErrorString(e));
   return MEP_OK;
