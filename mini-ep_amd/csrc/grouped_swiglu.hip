@@ -697,9 +697,10 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
           else mfma_acc(acc[i][j], fb[j], fa[SET][i]);
         }
         if constexpr (RD) {
+          // the next step's first group needs all four row fragments: read
+          // them in the first four groups (their own register set is free)
+          if (j < MF) fa[SET ^ 1][j] = *reinterpret_cast<const u32x4*>(R + a_base[RKK] + j * 16 * RB);
           fb[j] = *reinterpret_cast<const u32x4*>(R + b_base[RKK] + b_off(j));
-          if (j % 2 == 1)
-            fa[SET ^ 1][j / 2] = *reinterpret_cast<const u32x4*>(R + a_base[RKK] + (j / 2) * 16 * RB);
         }
         asm volatile("" ::: "memory");
       }
