@@ -620,6 +620,9 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
         }
         s.off[i] = src_row * static_cast<uint32_t>(K * 2) + lane_off;
       }
+      // a row half needs only A rows 0..127 (waves 0-1): the other A waves'
+      // loads read past a zero-sized buffer, i.e. zeros, without memory traffic
+      if (t.act_wm < 4 && wv * BPW * 8 >= t.act_wm * 64) s.bytes = 0;
     } else {
       s.base = static_cast<const unsigned char*>(p.W) + static_cast<int64_t>(t.e) * p.w_expert_stride * 2;
       s.bytes = static_cast<int>(p.w_expert_stride * 2);
@@ -636,6 +639,7 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
         else wrow0 = t.nt * BN + pair_cols(rb0);
         s.off[i] = static_cast<uint32_t>(wrow0 * K * 2) + lane_off;
       }
+      if (t.act_wm == 0) s.bytes = 0;          // empty half: nothing is computed
     }
     return s;
   };
@@ -770,6 +774,8 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
         u32x4 w;
 #pragma unroll
         for (int h = 0; h < 4; ++h) w[h] = pack_bf16x2(v[2 * h], v[2 * h + 1]);
+        // (non-temporal stores for GEMM-2's y rows were measured slower over
+        // the whole layer: the combine then reads them from HBM)
         if (ok) *reinterpret_cast<u32x4*>(dst + jp * 32) = w;
       }
     }
