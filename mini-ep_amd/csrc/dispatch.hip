@@ -153,18 +153,34 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(DispatchParams p) {
   if (tid == 0) flag = 0;
   __syncthreads();
 
-  // 1. segment totals and my prefix, from the per-block histograms
+  // 1. segment totals and my prefix, from the per-block histograms.  The
+  // histogram loads of a thread are issued 8 at a time before any of them is
+  // used (one L2 round trip per 8 blocks instead of one per block); with one
+  // segment the total is summed in a register and added to LDS once.
   {
     const int parts = kThreads / E > 0 ? kThreads / E : 1;
     const int e = tid % E, part = tid / E;
     if (part < parts && tid < parts * E) {
-      int my_pre = 0;
-      for (int bb = part; bb < p.nb; bb += parts) {
-        const int c = p.bc[static_cast<int64_t>(bb) * E + e];
-        const int sb = segment_of_block(p, bb);
-        atomicAdd(&segtot[sb][e], c);
-        if (sb == s && bb < b) my_pre += c;
+      int my_pre = 0, my_tot = 0;
+      constexpr int kBatch = 8;
+      for (int bb0 = part; bb0 < p.nb; bb0 += parts * kBatch) {
+        int c[kBatch];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+          const int bb = bb0 + u * parts;
+          c[u] = bb < p.nb ? p.bc[static_cast<int64_t>(bb) * E + e] : 0;
+        }
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+          const int bb = bb0 + u * parts;
+          if (bb >= p.nb) continue;
+          const int sb = p.n_seg == 1 ? 0 : segment_of_block(p, bb);
+          if (p.n_seg == 1) my_tot += c[u];
+          else atomicAdd(&segtot[sb][e], c[u]);
+          if (sb == s && bb < b) my_pre += c[u];
+        }
       }
+      if (p.n_seg == 1) atomicAdd(&segtot[0][e], my_tot);
       atomicAdd(&pre[e], my_pre);
     }
   }

@@ -123,6 +123,74 @@ __device__ void select_topk_from_lds(const float* lg, int ld, int rows, int E_rt
   }
 }
 
+// Top-KC of a 16 x EC tile (compile-time EC and KC, both multiples of 4) by
+// one wave, with no workgroup barrier: lane 4 t + g owns token t and experts
+// g*EC/4 .. (g+1)*EC/4 - 1.  Each lane writes its experts' 64-bit keys
+// (order_key << 32 | ~e, as in select_topk_from_lds) to the wave's LDS rows,
+// reads its token's whole row once, and ranks its own experts against it;
+// rank < KC goes to slot `rank`.  Then lane (t, g) writes slots
+// g*KC/4 .. of token t; the softmax is computed by every lane of the token in
+// the same order (max = slot 0, exp of differences summed in slot order), so
+// the gates equal the general path's bit for bit.  All data is wave-private,
+// so s_waitcnt on LDS orders it.
+template <int GATE_DT, int EC, int KC>
+__device__ void select_topk_wave(const float* lg, int ld, int64_t t0, int64_t n_tokens, float* sel_val,
+                                 int* sel_idx, int64_t* topk_idx, typename Elem<GATE_DT>::T* gate,
+                                 uint64_t* keys, int kld) {
+  static_assert(EC % 4 == 0 && KC % 4 == 0 && KC <= EC && kRowsPerWave * 4 == 64, "lane layout");
+  constexpr int EG = EC / 4, SG = KC / 4;
+  const int lane = lane_id();
+  const int t = lane >> 2, g = lane & 3;
+  float v[EG];
+  uint64_t ke[EG];
+#pragma unroll
+  for (int i = 0; i < EG; ++i) {
+    const int e = g * EG + i;
+    v[i] = lg[t * ld + e];
+    ke[i] = (static_cast<uint64_t>(order_key(v[i])) << 32) | static_cast<uint32_t>(~e);
+    keys[t * kld + e] = ke[i];
+  }
+  __builtin_amdgcn_s_waitcnt(0xC07F);            // lgkmcnt(0): the row is in LDS
+  __builtin_amdgcn_wave_barrier();
+  int rank[EG];
+#pragma unroll
+  for (int i = 0; i < EG; ++i) rank[i] = 0;
+  const uint64_t* row = keys + t * kld;
+#pragma unroll
+  for (int j2 = 0; j2 < EC / 2; ++j2) {
+    const u32x4 q = *reinterpret_cast<const u32x4*>(row + 2 * j2);
+    const uint64_t a = (static_cast<uint64_t>(q.y) << 32) | q.x;
+    const uint64_t b = (static_cast<uint64_t>(q.w) << 32) | q.z;
+#pragma unroll
+    for (int i = 0; i < EG; ++i) rank[i] += (a > ke[i]) + (b > ke[i]);
+  }
+#pragma unroll
+  for (int i = 0; i < EG; ++i) {
+    if (rank[i] < KC) {
+      sel_val[t * KC + rank[i]] = v[i];
+      sel_idx[t * KC + rank[i]] = g * EG + i;
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  __builtin_amdgcn_wave_barrier();
+  float sv[KC];
+#pragma unroll
+  for (int q = 0; q < KC / 4; ++q) {
+    const f32x4 w4 = *reinterpret_cast<const f32x4*>(sel_val + t * KC + 4 * q);
+    sv[4 * q] = w4.x; sv[4 * q + 1] = w4.y; sv[4 * q + 2] = w4.z; sv[4 * q + 3] = w4.w;
+  }
+  float ex[KC], sum = 0.0f;
+#pragma unroll
+  for (int q = 0; q < KC; ++q) { ex[q] = expf(sv[q] - sv[0]); sum += ex[q]; }
+  if (t0 + t < n_tokens) {
+#pragma unroll
+    for (int q = g * SG; q < (g + 1) * SG; ++q) {
+      topk_idx[(t0 + t) * KC + q] = sel_idx[t * KC + q];
+      gate[(t0 + t) * KC + q] = Elem<GATE_DT>::from_f32(ex[q] / sum);
+    }
+  }
+}
+
 // Logit tiles on the matrix cores.  A workgroup of kWaves waves owns
 // kWaves x 16 tokens; W_r is staged through LDS in K segments of at most
 // kSegBytes (all waves share it), x is streamed straight from HBM into the
@@ -228,7 +296,14 @@ __global__ __launch_bounds__(kWaves * 64) void router_kernel(const typename Elem
   for (int nf = 0; nf < NF; ++nf)
 #pragma unroll
     for (int i = 0; i < 4; ++i) lg[wave][4 * g + i][nf * 16 + r] = acc[nf][i];
-  __syncthreads();
+  constexpr bool kWaveSelect = KC > 0 && KC % 4 == 0 && E % 4 == 0;
+  if constexpr (kWaveSelect) {
+    // the tile is this wave's own: order the LDS writes before the reads
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_wave_barrier();
+  } else {
+    __syncthreads();
+  }
 
   if (logits != nullptr) {
     for (int p = lane; p < kRowsPerWave * E; p += 64) {
@@ -236,8 +311,12 @@ __global__ __launch_bounds__(kWaves * 64) void router_kernel(const typename Elem
       if (t0 + t < n_tokens) logits[(t0 + t) * E + (p - t * E)] = lg[wave][t][p - t * E];
     }
   }
-  select_topk_from_lds<DT, E, KC>(&lg[wave][0][0], E + 1, kRowsPerWave, E, k, t0, n_tokens, sel_val[wave],
-                                  sel_idx[wave], rsum[wave], topk_idx, gate, keys[wave], E + 2);
+  if constexpr (kWaveSelect)
+    select_topk_wave<DT, E, KC>(&lg[wave][0][0], E + 1, t0, n_tokens, sel_val[wave], sel_idx[wave], topk_idx, gate,
+                                keys[wave], E + 2);
+  else
+    select_topk_from_lds<DT, E, KC>(&lg[wave][0][0], E + 1, kRowsPerWave, E, k, t0, n_tokens, sel_val[wave],
+                                    sel_idx[wave], rsum[wave], topk_idx, gate, keys[wave], E + 2);
 }
 
 // Top-k + softmax of precomputed logits: one wave per `rows` tokens.
