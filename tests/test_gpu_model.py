@@ -20,7 +20,7 @@ sums run in different orders), grow through the layers and flip decisions
 whose top-2 logit gap is small.  The bar is therefore the model's own noise
 floor: the HIP path may differ from the reference in at most as many
 decisions as the reference differs from itself when +-1 ulp is injected into
-~40 % of its MoE outputs (max over 2 seeds, at least 4), and only where the
+~40 % of its MoE outputs (max over 4 seeds, at least 4), and only where the
 reference's top-2 gap is below MARGIN.
 """
 import time
@@ -88,10 +88,12 @@ def test_config3_greedy_identity():
     differ = toks != rtoks
     n_differ = int(differ.sum())
 
-    # the model's own noise floor: the reference against itself with +-1 ulp MoE noise
+    # the model's own noise floor: the reference against itself with +-1 ulp MoE
+    # noise, the largest count over 4 noise draws (2 draws were measured to
+    # scatter by a few decisions, enough to make the bound itself noisy)
     ref_free, _ = greedy_generate(ref, prompts, 32)
     floor = 0
-    for seed in range(2):
+    for seed in range(4):
         noisy = _ref_model(cfg, w, lambda i, b: _UlpNoise(b, 1000 * seed + i))
         ntoks, _ = greedy_generate(noisy, prompts, 32, forced=ref_free)
         floor = max(floor, int((ntoks != ref_free).sum()))
