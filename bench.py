@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """MoE-layer throughput of the GraniteMoE MoE block on one MI355X.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps 50] [--warmup 100] [--no-cpu-baseline]
 
 Workload: one bf16 MoE layer (hidden 1024, 32 experts, top-8, SwiGLU
 intermediate 512), T = 16384 tokens whose routing is Zipf(1.2)-skewed
@@ -54,8 +54,10 @@ PEAK_HBM_BYTES = 8.0e12       # MI355X HBM3E
 def parse_args(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=50)
+    # from an idle GPU the step runs 10-25 % slow for its first ~90 steps
+    # (~50 ms) while the clocks settle; the default warm-up covers that
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--tokens", type=int, default=16384)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-tokens", type=int, default=16384)

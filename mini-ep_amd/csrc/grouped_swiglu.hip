@@ -443,7 +443,12 @@ constexpr int BREGION = 2 * HALF;             // weight rows of both stages star
 constexpr int MF = 4, NF = 8;                 // 16 x 16 fragments per wave (64 x 128)
 constexpr int BPW = 8;                        // 1 KiB DMA blocks (8 rows x 128 B) per wave per stage
 constexpr int NLMAX = 256;
-constexpr int LDS_BYTES = 4 * HALF + (2 * (NLMAX + 1) + 2 * BM) * 4;
+// GEMM-2 output staging: 8 rows x 256 B (a wave's 128 columns) per wave,
+// after the stage buffers; the tables follow it
+constexpr int STG_ROWS = 8, STG_WAVE = STG_ROWS * 256, STG = 4 * HALF;
+constexpr int TABLES = STG + NW * STG_WAVE;
+constexpr int LDS_BYTES = TABLES + (2 * (NLMAX + 1) + 2 * BM) * 4;
+static_assert(LDS_BYTES <= 160 * 1024, "LDS budget of one workgroup");
 // buffer resource word 3 for raw 32-bit buffer access on gfx9-family parts
 constexpr int kBufWord3 = 0x00020000;
 static_assert(BN * RB == HALF, "A and weight rows of a stage are the same size");
@@ -489,7 +494,7 @@ template <bool GEMM1>
 __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
   using namespace bfk;
   __shared__ __attribute__((aligned(16))) unsigned char smem[LDS_BYTES];
-  int* const s_prefix = reinterpret_cast<int*>(smem + 4 * HALF);       // [NLMAX + 1] tiles before expert j
+  int* const s_prefix = reinterpret_cast<int*>(smem + TABLES);         // [NLMAX + 1] tiles before expert j
   int* const s_off = s_prefix + NLMAX + 1;                             // [NLMAX + 1] row offsets
   int* const s_rows = s_off + NLMAX + 1;                               // [2][BM] row maps
 
@@ -728,12 +733,13 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
   };
 
   // ---- epilogue -----------------------------------------------------------------------
-  // Straight from the accumulators to global memory: with the weight rows
-  // permuted per 32-column group (pair_cols), lane (lr, lg) of the fragment
-  // pair (2 jp, 2 jp + 1) in row fragment i holds 8 consecutive output columns
-  // of one row: one 16-byte store (16 rows x 64 contiguous bytes per
-  // instruction).  No LDS staging and no barrier: the stores drain while the
-  // next tile's MFMAs run.
+  // From the accumulators: with the weight rows permuted per 32-column group
+  // (pair_cols), lane (lr, lg) of the fragment pair (2 jp, 2 jp + 1) in row
+  // fragment i holds 8 consecutive output columns of one row.  GEMM-1 stores
+  // them directly (16 rows x 64 contiguous bytes per instruction; its SiLU
+  // keeps the VALU busier than the stores); GEMM-2 regroups them into whole
+  // lines through a per-wave LDS slice.  No workgroup barrier: the stores
+  // drain while the next tile's MFMAs run.
   typedef uint16_t T;
   T* const C = static_cast<T*>(p.C);
   constexpr int CN = GEMM1 ? BN / 2 : BN;     // output columns per tile
@@ -752,31 +758,66 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
     int et = tid;
     asm volatile("" : "+v"(et));
     const int elr = et & 15, elg = (et >> 4) & 3;
-    const int col = t.nt * CN + (GEMM1 ? wn * 64 : wn * 128) + elg * 8;   // first column of fragment pair 0
+    const int col0 = t.nt * CN + (GEMM1 ? wn * 64 : wn * 128);          // the wave's first output column
+    if constexpr (GEMM1) {
+      const int col = col0 + elg * 8;                                     // first column of fragment pair 0
 #pragma unroll
-    for (int i = 0; i < MF; ++i) {
-      const int r = wm * 64 + i * 16 + elr;
-      int64_t row;
-      if constexpr (GEMM1) row = t.row0 + r;
-      else row = s_rows[parity * BM + r];                                   // (token, slot) cell
-      T* const dst = C + row * p.N + col;
-      const bool ok = t.row0 + r < t.valid_end;
+      for (int i = 0; i < MF; ++i) {
+        const int r = wm * 64 + i * 16 + elr;
+        T* const dst = C + static_cast<int64_t>(t.row0 + r) * p.N + col;
+        const bool ok = t.row0 + r < t.valid_end;
 #pragma unroll
-      for (int jp = 0; jp < (GEMM1 ? NF / 4 : NF / 2); ++jp) {             // fragment pairs (2 jp, 2 jp + 1)
-        float v[8];
+        for (int jp = 0; jp < NF / 4; ++jp) {                               // fragment pairs (2 jp, 2 jp + 1)
+          float v[8];
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
+          for (int h = 0; h < 2; ++h)
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const int j = 2 * jp + h;
-            v[4 * h + q] = GEMM1 ? silu_f(acc[i][j][q]) * acc[i][j + NF / 2][q] : acc[i][j][q];
+            for (int q = 0; q < 4; ++q) v[4 * h + q] = silu_f(acc[i][2 * jp + h][q]) * acc[i][2 * jp + h + NF / 2][q];
+          u32x4 w;
+#pragma unroll
+          for (int h = 0; h < 4; ++h) w[h] = pack_bf16x2(v[2 * h], v[2 * h + 1]);
+          if (ok) *reinterpret_cast<u32x4*>(dst + jp * 32) = w;
+        }
+      }
+    } else {
+      // GEMM-2: lane (elr, elg) holds 16-byte chunk 4 jp + elg of row elr of
+      // each row fragment, i.e. 64 bytes of a row per store instruction.  The
+      // rows go through this wave's LDS slice instead (8 rows at a time,
+      // chunk c of row r at (c ^ r) * 16: conflict-free both ways) and leave
+      // as 4 rows x 256 contiguous bytes per store: whole 128-byte lines,
+      // which the memory system takes about twice as fast as half lines.
+      // The slice is private to the wave and a wave's LDS accesses complete
+      // in issue order, so no barrier or wait is needed around it.
+      unsigned char* const stg = smem + STG + wave * STG_WAVE;
+      const int lrow = (et >> 4) & 3, lchunk = et & 15;                    // read-back: row lrow (+4), chunk lchunk
+#pragma unroll
+      for (int i = 0; i < MF; ++i) {
+        u32x4 w[NF / 2];
+#pragma unroll
+        for (int jp = 0; jp < NF / 2; ++jp)
+#pragma unroll
+          for (int h = 0; h < 4; ++h)
+            w[jp][h] = pack_bf16x2(acc[i][2 * jp + h / 2][2 * (h & 1)], acc[i][2 * jp + h / 2][2 * (h & 1) + 1]);
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+          if ((elr >> 3) == half) {
+#pragma unroll
+            for (int jp = 0; jp < NF / 2; ++jp)
+              *reinterpret_cast<u32x4*>(stg + (elr & 7) * 256 + (((4 * jp + elg) ^ (elr & 7)) << 4)) = w[jp];
           }
-        u32x4 w;
+          asm volatile("" ::: "memory");
 #pragma unroll
-        for (int h = 0; h < 4; ++h) w[h] = pack_bf16x2(v[2 * h], v[2 * h + 1]);
-        // (non-temporal stores for GEMM-2's y rows were measured slower over
-        // the whole layer: the combine then reads them from HBM)
-        if (ok) *reinterpret_cast<u32x4*>(dst + jp * 32) = w;
+          for (int sr = 0; sr < 2; ++sr) {
+            const int rr = 4 * sr + lrow;                                    // row of the slice
+            const u32x4 v = *reinterpret_cast<const u32x4*>(stg + rr * 256 + ((lchunk ^ rr) << 4));
+            const int r = wm * 64 + i * 16 + 8 * half + rr;
+            const int64_t row = s_rows[parity * BM + r];                     // (token, slot) cell
+            // (non-temporal stores for the y rows were measured slower over
+            // the whole layer: the combine then reads them from HBM)
+            if (t.row0 + r < t.valid_end) *reinterpret_cast<u32x4*>(C + row * p.N + col0 + lchunk * 8) = v;
+          }
+          asm volatile("" ::: "memory");
+        }
       }
     }
   };
