@@ -403,8 +403,8 @@ hipError_t launch(const GemmParams& p, int64_t max_rows, hipStream_t stream) {
 }
 
 // ============================================================================
-// bf16 path: 8 waves, two 64 KiB LDS stages of two K-steps each, AGPR
-// accumulators.
+// bf16 path: 8 waves, two 64 KiB LDS stages of two K-steps each, inline-asm
+// MFMAs with VGPR accumulators.
 //
 // Tile 256 x 256 (GEMM-1: 128 gate + 128 up columns), 8 waves (4 x 2) of
 // 64 x 128.  One MFMA step covers 32 of K; a stage holds two steps (128 bytes
@@ -424,12 +424,14 @@ hipError_t launch(const GemmParams& p, int64_t max_rows, hipStream_t stream) {
 // So a stage's DMA has two steps to land, and there is one barrier per stage.
 // MFMAs run column-major (the 4 MFMAs of weight fragment j, then j+1): row
 // fragments are double-buffered, weight fragment j is refilled right after its
-// group.  The MFMAs are inline asm with "+a" accumulators, which keeps the 128
-// accumulators in AGPRs (with the builtin the compiler moves them between
+// group.  The MFMAs are inline asm with "+v" accumulators: the 128
+// accumulators stay in arch VGPRs next to everything else (226-244 of the 256
+// a wave has at two waves per SIMD), so the epilogue reads them without 128
+// v_accvgpr_read moves (with the builtin the compiler moves them between
 // register files and spills).
 //
-// Epilogue straight from the accumulators (16-byte stores, see pair_cols), no
-// LDS and no barrier.  The K order of a tile is rotated by its column-tile
+// Epilogue straight from the accumulators (16-byte stores, see pair_cols;
+// GEMM-2 regroups them into whole lines in LDS), no workgroup barrier.  The K order of a tile is rotated by its column-tile
 // index (n_tile * KD / 4 stages), which spreads the tiles running at the same
 // time over more memory channels; the rotation depends only on the output
 // columns, so every output element is summed in the same order wherever its
@@ -456,19 +458,19 @@ static_assert((BM + BN) / 8 == NW * BPW, "DMA blocks cover the stage");
 static_assert(BPW == NF, "one DMA block per MFMA group of an odd step");
 }  // namespace bfk
 
-// 16x16x32 bf16 MFMA with the accumulator pinned to AGPRs; src0 = weight
+// 16x16x32 bf16 MFMA with the accumulator in VGPRs; src0 = weight
 // fragment, src1 = row fragment, so the result is C^T (lane: one row, 4
 // consecutive columns).  mfma_first starts a new accumulation (C operand 0).
 __device__ __forceinline__ void mfma_acc(f32x4& acc, const u32x4& w, const u32x4& a) {
-  asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(w), "v"(a));
+  asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+v"(acc) : "v"(w), "v"(a));
 }
 __device__ __forceinline__ void mfma_first(f32x4& acc, const u32x4& w, const u32x4& a) {
-  asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, 0" : "=a"(acc) : "v"(w), "v"(a));
+  asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, 0" : "=v"(acc) : "v"(w), "v"(a));
 }
 // Orders later reads of `acc` after every earlier volatile asm (an empty asm
-// that claims to rewrite it).  AMDGPU constraints live in device functions
-// only: in a kernel body the host pass would parse "a" as an x86 register.
-__device__ __forceinline__ void pin_acc(f32x4& acc) { asm volatile("" : "+a"(acc)); }
+// that claims to rewrite it).  AMDGPU register constraints live in device
+// functions only: in a kernel body the host pass parses them as x86 ones.
+__device__ __forceinline__ void pin_acc(f32x4& acc) { asm volatile("" : "+v"(acc)); }
 // buffer_load_dwordx4 ... lds of one 1 KiB block: lane L's 16 bytes from
 // base + voff + soff land at lds + 16 L; an offset at or past `bytes` reads
 // zeros instead of faulting.  (A plain device function: inside the kernel
@@ -745,7 +747,7 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
   constexpr int CN = GEMM1 ? BN / 2 : BN;     // output columns per tile
   auto epilogue = [&](const Tile& t, int parity) {
     if (wm >= t.act_wm) return;
-    // the last MFMAs' results must be written before the AGPRs are read (the
+    // the last MFMAs' results must be written before they are read (the
     // asm hides the MFMAs from the hazard recognizer): pad, then tie every
     // accumulator to an (empty) asm after the padding so no read moves above it
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
