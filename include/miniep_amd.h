@@ -144,6 +144,11 @@ int mep_dispatch_check(const void* workspace, void* stream);
  *   x (N, H)   w_in (n_local, 2I, H)   w_out (n_local, H, I)   y_entries (N*k, H)
  * max_rows >= offsets[n_local] (e.g. N*k) bounds the launch.
  * Supported: H % 256 == 0, I % 128 == 0.
+ * tile_queue: 2 int32 of device memory that are zero before the first call;
+ * the bf16 kernels hand out their last round of tiles through them and every
+ * launch leaves them zero again.  Launches that may run at the same time (on
+ * different streams) need different queues; launches on one stream can share
+ * one.  No counterpart in the reference (its experts are a Python loop).
  * ---------------------------------------------------------------------- */
 size_t mep_experts_workspace_size(int64_t max_rows, int32_t inter, int32_t dtype);
 
@@ -151,7 +156,7 @@ int mep_grouped_swiglu(const void* x, int64_t n_tokens, int32_t top_k,
                        const int32_t* perm, const int32_t* offsets, int32_t n_local,
                        int64_t max_rows, const void* w_in, const void* w_out,
                        int32_t hidden, int32_t inter, int32_t dtype, void* y_entries,
-                       void* workspace, size_t workspace_bytes, void* stream);
+                       void* workspace, size_t workspace_bytes, int32_t* tile_queue, void* stream);
 
 /* The two launches of mep_grouped_swiglu as separate calls, for callers that
  * schedule or time them individually (same kernels, same results):
@@ -162,12 +167,12 @@ int mep_grouped_swiglu(const void* x, int64_t n_tokens, int32_t top_k,
 int mep_swiglu_gate_up(const void* x, int64_t n_tokens, int32_t top_k, const int32_t* perm,
                        const int32_t* offsets, int32_t n_local, int64_t max_rows,
                        const void* w_in, int32_t hidden, int32_t inter, int32_t dtype,
-                       void* act, size_t act_bytes, void* stream);
+                       void* act, size_t act_bytes, int32_t* tile_queue, void* stream);
 
 int mep_swiglu_down(const void* act, int64_t n_tokens, int32_t top_k, const int32_t* perm,
                     const int32_t* offsets, int32_t n_local, int64_t max_rows,
                     const void* w_out, int32_t hidden, int32_t inter, int32_t dtype,
-                    void* y_entries, void* stream);
+                    void* y_entries, int32_t* tile_queue, void* stream);
 
 /* ------------------------------------------------------------------------
  * Combine: out[t] = sum_{s=0..k-1, row_of_entry[t*k+s] >= 0} gate[t,s] * y_entries[t*k+s]

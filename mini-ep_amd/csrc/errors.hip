@@ -18,4 +18,4 @@ void clear_error() { g_last_error[0] = '\0'; }
 
 extern "C" const char* mep_last_error(void) { return mep::g_last_error; }
 
-extern "C" int mep_abi_version(void) { return 1; }
+extern "C" int mep_abi_version(void) { return 2; }

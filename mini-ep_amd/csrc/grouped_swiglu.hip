@@ -71,6 +71,7 @@ struct GemmParams {
   uint32_t a_bytes;          // size of A in bytes (< 4 GiB)
   uint32_t k_magic;          // entry / top_k == umulhi(entry, k_magic) >> k_shift for entry < 2^31
   int k_shift;
+  int* tile_queue;           // bf16 kernels: 2 counters, zero before and after every launch
 };
 
 // Round-up reciprocal for exact division by d of every n < 2^31: with
@@ -449,7 +450,7 @@ constexpr int NLMAX = 256;
 // after the stage buffers; the tables follow it
 constexpr int STG_ROWS = 8, STG_WAVE = STG_ROWS * 256, STG = 4 * HALF;
 constexpr int TABLES = STG + NW * STG_WAVE;
-constexpr int LDS_BYTES = TABLES + (2 * (NLMAX + 1) + 2 * BM) * 4;
+constexpr int LDS_BYTES = TABLES + (2 * (NLMAX + 1) + 2 * BM + 2) * 4;
 static_assert(LDS_BYTES <= 160 * 1024, "LDS budget of one workgroup");
 // buffer resource word 3 for raw 32-bit buffer access on gfx9-family parts
 constexpr int kBufWord3 = 0x00020000;
@@ -499,6 +500,7 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
   int* const s_prefix = reinterpret_cast<int*>(smem + TABLES);         // [NLMAX + 1] tiles before expert j
   int* const s_off = s_prefix + NLMAX + 1;                             // [NLMAX + 1] row offsets
   int* const s_rows = s_off + NLMAX + 1;                               // [2][BM] row maps
+  int* const s_pool = s_rows + 2 * BM;                                 // [2] pool items taken
 
   const int tid = threadIdx.x;
   // wave index as a scalar: keeps per-wave choices (A or weight rows, buffer
@@ -521,25 +523,38 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
     for (int j = 0; j < nl; ++j) s_prefix[j + 1] += s_prefix[j];
   __syncthreads();
   const int total = __builtin_amdgcn_readfirstlane(s_prefix[nl]);
-  // Work items.  XCD x owns tiles [x_lo, x_hi); its nslots workgroups take
-  // items slot, slot + nslots, ...  When the XCD's tile count leaves a
-  // remainder L <= nslots / 2 after whole rounds, its first L tiles are split
-  // into 2 L row halves (128 rows each) that come first, one per workgroup, so
-  // the last round does not leave most workgroups idle.  A row half sums every
-  // output element in the same order as the whole tile.
+  // Work items.  XCD x owns tiles [lo(x), hi(x)); its nslots workgroups take
+  // items slot, slot + nslots, ... for the n_priv whole rounds.  The tiles
+  // left over after the whole rounds of every XCD form one pool (XCD 0's,
+  // then XCD 1's, ...) that workgroups take one at a time through an atomic
+  // counter once their own rounds are done, so the last round goes to
+  // whichever workgroups finish first instead of a fixed, possibly slow,
+  // subset.  Which workgroup computes a tile does not change its result.
   const int per_xcd = (total + 7) / 8;
   const int xcd = blockIdx.x % 8, slot = blockIdx.x / 8, nslots = gridDim.x / 8;
-  const int x_lo = min(total, xcd * per_xcd), x_hi = min(total, x_lo + per_xcd);
-  const int rem = (x_hi - x_lo) % nslots;
-  const int n_half = (2 * rem <= nslots) ? 2 * rem : 0;
-  const int n_items = x_hi - x_lo + n_half / 2;
-  const int n_my = slot < n_items ? (n_items - slot + nslots - 1) / nslots : 0;
-  auto tile_valid = [&](int i) { return i < n_my; };
-  if (!tile_valid(0)) return;
+  auto xcd_lo = [&](int x) { return min(total, x * per_xcd); };
+  auto xcd_rem = [&](int x) { return (min(total, x * per_xcd + per_xcd) - xcd_lo(x)) % nslots; };
+  const int x_lo = xcd_lo(xcd);
+  const int n_priv = (min(total, x_lo + per_xcd) - x_lo) / nslots;
+  int pool_size = 0;
+  for (int x = 0; x < 8; ++x) pool_size += xcd_rem(x);
+  pool_size = __builtin_amdgcn_readfirstlane(pool_size);
+  auto pool_tile = [&](int g) {                  // g < pool_size
+    int x = 0;
+    for (; x < 7; ++x) {
+      const int r = xcd_rem(x);
+      if (g < r) break;
+      g -= r;
+    }
+    return min(total, x * per_xcd + per_xcd) - xcd_rem(x) + g;
+  };
+  int* const queue = p.tile_queue;               // [0]: pool items taken, [1]: workgroups done
 
   // row0 .. row0+255: the rows a tile computes (loads clamp to row_end - 1);
   // rows at or past valid_end are not stored; waves with wm >= act_wm compute
-  // nothing (a row half runs on the 4 waves of rows 0..127, one per SIMD).
+  // nothing.  A tile with at most 128 rows (an expert's last, partial one) is
+  // a row half: the 4 waves of rows 0..127, one per SIMD, compute it, and a
+  // row half sums every output element in the same order as a whole tile.
   struct Tile { int e, row0, row_end, valid_end, nt, act_wm; };
   auto decode_tile = [&](int lt) {
     int lo = 0, hi = nl - 1;                       // largest j with s_prefix[j] <= lt
@@ -554,24 +569,11 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
     t.row_end = __builtin_amdgcn_readfirstlane(s_off[lo + 1]);
     t.nt = __builtin_amdgcn_readfirstlane(u % p.n_tiles_n);
     t.valid_end = t.row_end;
-    t.act_wm = 4;
+    t.act_wm = (t.row_end - t.row0 <= BM / 2) ? 2 : 4;
     return t;
   };
-  auto decode = [&](int i) {
-    const int u = slot + i * nslots;
-    if (u >= n_half) return decode_tile(x_lo + n_half / 2 + (u - n_half));
-    Tile t = decode_tile(x_lo + u / 2);
-    const int r0 = t.row0 + (u & 1) * (BM / 2);
-    if (r0 < t.row_end) {
-      t.row0 = r0;
-      t.valid_end = min(t.row_end, r0 + BM / 2);
-      t.act_wm = 2;
-    } else {                                   // empty half: addresses of the tile, nothing computed
-      t.valid_end = t.row0;
-      t.act_wm = 0;
-    }
-    return t;
-  };
+  // item i of this workgroup: a tile of its own rounds, or pool item g
+  auto decode = [&](int i, int g) { return decode_tile(i < n_priv ? x_lo + slot + i * nslots : pool_tile(g)); };
   // row map: perm[row0 .. row0 + BM) of a tile DMA'd into LDS (clamped to the
   // tile's last row, so every lane reads inside perm).  GEMM-1 gathers its A
   // rows through it, GEMM-2 scatters its output rows.
@@ -646,7 +648,6 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
         else wrow0 = t.nt * BN + pair_cols(rb0);
         s.off[i] = static_cast<uint32_t>(wrow0 * K * 2) + lane_off;
       }
-      if (t.act_wm == 0) s.bytes = 0;          // empty half: nothing is computed
     }
     return s;
   };
@@ -825,63 +826,102 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
   };
 
   // ---- persistent step loop ---------------------------------------------------------
-  Tile cur = decode(0);
-  bool has_next = tile_valid(1);
-  Tile nxt = has_next ? decode(1) : cur;
-  rowmap_dma(cur, 0);
-  if (has_next) rowmap_dma(nxt, 1);
-  __builtin_amdgcn_s_waitcnt(kVmcnt0);
-  lds_barrier();
-  Src sc = setup(cur, 0);
+  // Items 0 and 1 are needed before the loop: with fewer than two own rounds
+  // they come from the pool now.  `pool_open`: no pool request of this
+  // workgroup has come back empty yet.
+  if (tid == 0) {
+    int g0 = pool_size, g1 = pool_size;
+    if (n_priv == 0) g0 = atomicAdd(queue, 1);
+    if (n_priv == 1 || (n_priv == 0 && g0 < pool_size)) g1 = atomicAdd(queue, 1);
+    s_pool[0] = g0;
+    s_pool[1] = g1;
+  }
+  __syncthreads();
+  const int g0 = __builtin_amdgcn_readfirstlane(s_pool[0]), g1 = __builtin_amdgcn_readfirstlane(s_pool[1]);
+  if (n_priv >= 1 || g0 < pool_size) {
+    Tile cur = decode(0, g0);
+    bool has_next = n_priv >= 2 || g1 < pool_size;
+    bool pool_open = has_next;
+    Tile nxt = has_next ? decode(1, g1) : cur;
+    rowmap_dma(cur, 0);
+    if (has_next) rowmap_dma(nxt, 1);
+    __builtin_amdgcn_s_waitcnt(kVmcnt0);
+    lds_barrier();
+    Src sc = setup(cur, 0);
 #pragma unroll
-  for (int i = 0; i < BPW; ++i) dma_blk(sc, 0, 0, i);
+    for (int i = 0; i < BPW; ++i) dma_blk(sc, 0, 0, i);
 #pragma unroll
-  for (int i = 0; i < BPW; ++i) dma_blk(sc, 1, 1, i);
-  __builtin_amdgcn_s_waitcnt(kVmcnt0);
-  lds_barrier();
+    for (int i = 0; i < BPW; ++i) dma_blk(sc, 1, 1, i);
+    __builtin_amdgcn_s_waitcnt(kVmcnt0);
+    lds_barrier();
 
-  std::integral_constant<int, 0> S0;
-  std::integral_constant<int, 1> S1;
-  std::integral_constant<bool, false> NO;
-  std::integral_constant<bool, true> YES;
-  // Invariant at a tile's start: its stages 0 and 1 are in buffers 0 and 1
-  // (landed, published).  Steps are unrolled by four (two stages), so every
-  // buffer index is an immediate.
-  for (int it = 0;; ++it) {
-    const bool act = wm < cur.act_wm;
-    if (act) first_frags();
-    step(S0, YES, NO, YES, sc, 0, 0, 0, act);          // step 0 (stage 0)
-    // every wave is past its previous epilogue (barrier above), so the row
-    // map buffer that epilogue read can take the next tile's row map; the
-    // wait at the end of step 2 covers it, setup() reads it at step KT-3
-    if (it > 0 && has_next) rowmap_dma(nxt, (it + 1) & 1);
-    step(S1, NO, YES, YES, sc, 2, 0, 1, act);          // step 1: DMA stage 2 -> buffer 0
-    step(S0, NO, NO, YES, sc, 0, 0, 1, act);           // step 2 (stage 1)
-    step(S1, NO, YES, YES, sc, 3, 1, 0, act);          // step 3: DMA stage 3 -> buffer 1
-    // steady state: steps k4 .. k4+3 (stages k4/2, k4/2 + 1) DMA stages k4/2 + 2, + 3
-    for (int k4 = 4; k4 < KT - 4; k4 += 4) {
-      step(S0, NO, NO, YES, sc, 0, 0, 0, act);
-      step(S1, NO, YES, YES, sc, k4 / 2 + 2, 0, 1, act);
-      step(S0, NO, NO, YES, sc, 0, 0, 1, act);
-      step(S1, NO, YES, YES, sc, k4 / 2 + 3, 1, 0, act);
+    std::integral_constant<int, 0> S0;
+    std::integral_constant<int, 1> S1;
+    std::integral_constant<bool, false> NO;
+    std::integral_constant<bool, true> YES;
+    // Invariant at a tile's start: its stages 0 and 1 are in buffers 0 and 1
+    // (landed, published).  Steps are unrolled by four (two stages), so every
+    // buffer index is an immediate.
+    for (int it = 0;; ++it) {
+      const bool act = wm < cur.act_wm;
+      // item it + 2 from the pool: requested after step 0, its answer lands
+      // before the wait at the end of step 2, goes to LDS after that step and
+      // is read by every wave at the end of this tile (barriers in between)
+      const bool grab = it + 2 >= n_priv && pool_open;
+      if (act) first_frags();
+      step(S0, YES, NO, YES, sc, 0, 0, 0, act);          // step 0 (stage 0)
+      // every wave is past its previous epilogue (barrier above), so the row
+      // map buffer that epilogue read can take the next tile's row map; the
+      // wait at the end of step 2 covers it, setup() reads it at step KT-3
+      if (it > 0 && has_next) rowmap_dma(nxt, (it + 1) & 1);
+      int got = 0;
+      if (grab && tid == 0) got = atomicAdd(queue, 1);
+      step(S1, NO, YES, YES, sc, 2, 0, 1, act);          // step 1: DMA stage 2 -> buffer 0
+      step(S0, NO, NO, YES, sc, 0, 0, 1, act);           // step 2 (stage 1)
+      if (grab && tid == 0) s_pool[0] = got;
+      step(S1, NO, YES, YES, sc, 3, 1, 0, act);          // step 3: DMA stage 3 -> buffer 1
+      // steady state: steps k4 .. k4+3 (stages k4/2, k4/2 + 1) DMA stages k4/2 + 2, + 3
+      for (int k4 = 4; k4 < KT - 4; k4 += 4) {
+        step(S0, NO, NO, YES, sc, 0, 0, 0, act);
+        step(S1, NO, YES, YES, sc, k4 / 2 + 2, 0, 1, act);
+        step(S0, NO, NO, YES, sc, 0, 0, 1, act);
+        step(S1, NO, YES, YES, sc, k4 / 2 + 3, 1, 0, act);
+      }
+      // last two stages: their odd steps DMA the next tile's stages 0 and 1.
+      // Without a next tile they re-read this tile's (in bounds, never consumed)
+      // so the code has no branch here.
+      step(S0, NO, NO, YES, sc, 0, 0, 0, act);           // step KT-4
+      sc = has_next ? setup(nxt, (it + 1) & 1) : setup(cur, it & 1);
+      step(S1, NO, YES, YES, sc, 0, 0, 1, act);          // step KT-3: next stage 0 -> buffer 0
+      step(S0, NO, NO, YES, sc, 0, 0, 1, act);           // step KT-2
+      step(S1, NO, YES, NO, sc, 1, 1, 0, act);           // step KT-1: next stage 1 -> buffer 1
+      epilogue(cur, it & 1);
+      if (!has_next) {
+        // no DMA may still be writing this workgroup's LDS when its waves end
+        __builtin_amdgcn_s_waitcnt(kVmcnt0);
+        break;
+      }
+      cur = nxt;
+      if (it + 2 < n_priv) {
+        nxt = decode(it + 2, 0);
+      } else if (grab) {
+        const int g = __builtin_amdgcn_readfirstlane(s_pool[0]);
+        has_next = pool_open = g < pool_size;
+        if (has_next) nxt = decode(it + 2, g);
+      } else {
+        has_next = false;
+      }
     }
-    // last two stages: their odd steps DMA the next tile's stages 0 and 1.
-    // Without a next tile they re-read this tile's (in bounds, never consumed)
-    // so the code has no branch here.
-    step(S0, NO, NO, YES, sc, 0, 0, 0, act);           // step KT-4
-    sc = has_next ? setup(nxt, (it + 1) & 1) : setup(cur, it & 1);
-    step(S1, NO, YES, YES, sc, 0, 0, 1, act);          // step KT-3: next stage 0 -> buffer 0
-    step(S0, NO, NO, YES, sc, 0, 0, 1, act);           // step KT-2
-    step(S1, NO, YES, NO, sc, 1, 1, 0, act);           // step KT-1: next stage 1 -> buffer 1
-    epilogue(cur, it & 1);
-    if (!has_next) {
-      // no DMA may still be writing this workgroup's LDS when its waves end
-      __builtin_amdgcn_s_waitcnt(kVmcnt0);
-      break;
+  }
+  // The pool counter returns to zero for the next launch: the last workgroup
+  // to get here resets it (every request of every workgroup has come back by
+  // then, and each workgroup arrives exactly once).
+  if (tid == 0) {
+    const int done = atomicAdd(queue + 1, 1);
+    if (done == static_cast<int>(gridDim.x) - 1) {
+      atomicExch(queue, 0);
+      atomicExch(queue + 1, 0);
     }
-    cur = nxt;
-    has_next = tile_valid(it + 2);
-    if (has_next) nxt = decode(it + 2);
   }
 }
 
@@ -911,9 +951,9 @@ typedef TileCfg<128, 128, 2, 2> CfgF32;
 template <int DT, class Cfg>
 int run_gate_up(const void* x, int64_t n_tokens, int top_k, const int32_t* perm, const int32_t* offsets,
                 int n_local, int64_t max_rows, const void* w_in, int hidden, int inter, void* act,
-                hipStream_t stream) {
+                int32_t* tile_queue, hipStream_t stream) {
   GemmParams g1;
-  g1.A = x; g1.perm = perm; g1.offsets = offsets; g1.W = w_in; g1.C = act;
+  g1.A = x; g1.perm = perm; g1.offsets = offsets; g1.W = w_in; g1.C = act; g1.tile_queue = tile_queue;
   g1.w_expert_stride = static_cast<int64_t>(2) * inter * hidden;
   g1.n_local = n_local; g1.top_k = top_k; g1.K = hidden; g1.N = inter;
   g1.n_tiles_n = inter / (Cfg::BN / 2);
@@ -928,9 +968,10 @@ int run_gate_up(const void* x, int64_t n_tokens, int top_k, const int32_t* perm,
 
 template <int DT, class Cfg>
 int run_down(const void* act, int top_k, const int32_t* perm, const int32_t* offsets, int n_local,
-             int64_t max_rows, const void* w_out, int hidden, int inter, void* y, hipStream_t stream) {
+             int64_t max_rows, const void* w_out, int hidden, int inter, void* y, int32_t* tile_queue,
+             hipStream_t stream) {
   GemmParams g2;
-  g2.A = act; g2.perm = perm; g2.offsets = offsets; g2.W = w_out; g2.C = y;
+  g2.A = act; g2.perm = perm; g2.offsets = offsets; g2.W = w_out; g2.C = y; g2.tile_queue = tile_queue;
   g2.w_expert_stride = static_cast<int64_t>(hidden) * inter;
   g2.n_local = n_local; g2.top_k = top_k; g2.K = inter; g2.N = hidden;
   g2.n_tiles_n = hidden / Cfg::BN;
@@ -975,12 +1016,14 @@ using namespace mep;
 extern "C" int mep_swiglu_gate_up(const void* x, int64_t n_tokens, int32_t top_k,
                                   const int32_t* perm, const int32_t* offsets, int32_t n_local,
                                   int64_t max_rows, const void* w_in, int32_t hidden, int32_t inter,
-                                  int32_t dtype, void* act, size_t act_bytes, void* stream) {
+                                  int32_t dtype, void* act, size_t act_bytes, int32_t* tile_queue,
+                                  void* stream) {
   clear_error();
   int rc = check_expert_args("mep_swiglu_gate_up", n_tokens, top_k, n_local, max_rows, hidden, inter, dtype);
   if (rc != MEP_OK) return rc;
   if (max_rows == 0 || n_local == 0) return MEP_OK;
-  MEP_REQUIRE(x && perm && offsets && w_in && act, MEP_ERR_INVALID_ARG, "mep_swiglu_gate_up: null pointer");
+  MEP_REQUIRE(x && perm && offsets && w_in && act && tile_queue, MEP_ERR_INVALID_ARG,
+              "mep_swiglu_gate_up: null pointer");
   const size_t need = static_cast<size_t>(max_rows) * inter * dtype_bytes(dtype);
   MEP_REQUIRE(act_bytes >= need, MEP_ERR_WORKSPACE, "mep_swiglu_gate_up: act %zu B < required %zu B",
               act_bytes, need);
@@ -989,29 +1032,29 @@ extern "C" int mep_swiglu_gate_up(const void* x, int64_t n_tokens, int32_t top_k
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == MEP_DTYPE_BF16)
     return run_gate_up<MEP_DTYPE_BF16, CfgBf16>(x, n_tokens, top_k, perm, offsets, n_local, max_rows, w_in,
-                                                hidden, inter, act, s);
+                                                hidden, inter, act, tile_queue, s);
   return run_gate_up<MEP_DTYPE_F32, CfgF32>(x, n_tokens, top_k, perm, offsets, n_local, max_rows, w_in, hidden,
-                                            inter, act, s);
+                                            inter, act, tile_queue, s);
 }
 
 extern "C" int mep_swiglu_down(const void* act, int64_t n_tokens, int32_t top_k, const int32_t* perm,
                                const int32_t* offsets, int32_t n_local, int64_t max_rows,
                                const void* w_out, int32_t hidden, int32_t inter, int32_t dtype,
-                               void* y_entries, void* stream) {
+                               void* y_entries, int32_t* tile_queue, void* stream) {
   clear_error();
   int rc = check_expert_args("mep_swiglu_down", n_tokens, top_k, n_local, max_rows, hidden, inter, dtype);
   if (rc != MEP_OK) return rc;
   if (max_rows == 0 || n_local == 0) return MEP_OK;
-  MEP_REQUIRE(act && perm && offsets && w_out && y_entries, MEP_ERR_INVALID_ARG,
+  MEP_REQUIRE(act && perm && offsets && w_out && y_entries && tile_queue, MEP_ERR_INVALID_ARG,
               "mep_swiglu_down: null pointer");
   MEP_REQUIRE(aligned16(act) && aligned16(w_out) && aligned16(y_entries), MEP_ERR_INVALID_ARG,
               "mep_swiglu_down: buffers must be 16-byte aligned");
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == MEP_DTYPE_BF16)
     return run_down<MEP_DTYPE_BF16, CfgBf16>(act, top_k, perm, offsets, n_local, max_rows, w_out, hidden,
-                                             inter, y_entries, s);
+                                             inter, y_entries, tile_queue, s);
   return run_down<MEP_DTYPE_F32, CfgF32>(act, top_k, perm, offsets, n_local, max_rows, w_out, hidden, inter,
-                                         y_entries, s);
+                                         y_entries, tile_queue, s);
 }
 
 extern "C" size_t mep_experts_workspace_size(int64_t max_rows, int32_t inter, int32_t dtype) {
@@ -1024,7 +1067,8 @@ extern "C" int mep_grouped_swiglu(const void* x, int64_t n_tokens, int32_t top_k
                                   const int32_t* perm, const int32_t* offsets, int32_t n_local,
                                   int64_t max_rows, const void* w_in, const void* w_out,
                                   int32_t hidden, int32_t inter, int32_t dtype, void* y_entries,
-                                  void* workspace, size_t workspace_bytes, void* stream) {
+                                  void* workspace, size_t workspace_bytes, int32_t* tile_queue,
+                                  void* stream) {
   clear_error();
   int rc = check_expert_args("mep_grouped_swiglu", n_tokens, top_k, n_local, max_rows, hidden, inter, dtype);
   if (rc != MEP_OK) return rc;
@@ -1034,8 +1078,8 @@ extern "C" int mep_grouped_swiglu(const void* x, int64_t n_tokens, int32_t top_k
   MEP_REQUIRE(workspace_bytes >= need, MEP_ERR_WORKSPACE,
               "mep_grouped_swiglu: workspace %zu B < required %zu B", workspace_bytes, need);
   rc = mep_swiglu_gate_up(x, n_tokens, top_k, perm, offsets, n_local, max_rows, w_in, hidden, inter, dtype,
-                          workspace, workspace_bytes, stream);
+                          workspace, workspace_bytes, tile_queue, stream);
   if (rc != MEP_OK) return rc;
   return mep_swiglu_down(workspace, n_tokens, top_k, perm, offsets, n_local, max_rows, w_out, hidden, inter,
-                         dtype, y_entries, stream);
+                         dtype, y_entries, tile_queue, stream);
 }

@@ -63,11 +63,11 @@ _SIGNATURES = {
     "mep_experts_workspace_size": (_size, [_i64, _i32, _i32]),
     "mep_grouped_swiglu": (ctypes.c_int, [_c_void_p, _i64, _i32, _c_void_p, _c_void_p, _i32,
                                           _i64, _c_void_p, _c_void_p, _i32, _i32, _i32,
-                                          _c_void_p, _c_void_p, _size, _c_void_p]),
+                                          _c_void_p, _c_void_p, _size, _c_void_p, _c_void_p]),
     "mep_swiglu_gate_up": (ctypes.c_int, [_c_void_p, _i64, _i32, _c_void_p, _c_void_p, _i32, _i64,
-                                          _c_void_p, _i32, _i32, _i32, _c_void_p, _size, _c_void_p]),
+                                          _c_void_p, _i32, _i32, _i32, _c_void_p, _size, _c_void_p, _c_void_p]),
     "mep_swiglu_down": (ctypes.c_int, [_c_void_p, _i64, _i32, _c_void_p, _c_void_p, _i32, _i64,
-                                       _c_void_p, _i32, _i32, _i32, _c_void_p, _c_void_p]),
+                                       _c_void_p, _i32, _i32, _i32, _c_void_p, _c_void_p, _c_void_p]),
     "mep_combine": (ctypes.c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i32,
                                    _i32, _i32, _c_void_p, _c_void_p]),
     "mep_gather_rows": (ctypes.c_int, [_c_void_p, _i64, _i32, _c_void_p, _i64, _i32, _i32, _c_void_p,

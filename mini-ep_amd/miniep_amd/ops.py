@@ -46,6 +46,20 @@ def _stream(dev: torch.device) -> int:
     return torch.cuda.current_stream(dev).cuda_stream
 
 
+_QUEUES: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def _tile_queue(dev: torch.device) -> torch.Tensor:
+    """Tile-queue counters of the grouped GEMMs for the current stream of
+    ``dev``: zeroed once here, left at zero by every launch, and one per stream
+    so that launches on different streams never share counters."""
+    key = (dev.index if dev.index is not None else torch.cuda.current_device(), _stream(dev))
+    q = _QUEUES.get(key)
+    if q is None:
+        q = _QUEUES[key] = torch.zeros(2, dtype=torch.int32, device=dev)
+    return q
+
+
 def _mask_u8(valid_mask: torch.Tensor | None, n: int) -> torch.Tensor | None:
     if valid_mask is None:
         return None
@@ -194,7 +208,8 @@ def grouped_swiglu(x_flat: torch.Tensor, disp: Dispatch, w_in: torch.Tensor, w_o
     ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
     rc = L.mep_grouped_swiglu(x.data_ptr(), n, disp.top_k, disp.perm.data_ptr(), disp.offsets.data_ptr(),
                               disp.n_local, max_rows, wi.data_ptr(), wo.data_ptr(), h, inter, code,
-                              y_entries.data_ptr(), ws.data_ptr(), ws.numel(), _stream(dev))
+                              y_entries.data_ptr(), ws.data_ptr(), ws.numel(), _tile_queue(dev).data_ptr(),
+                              _stream(dev))
     _lib.check(rc, "mep_grouped_swiglu")
     return y_entries
 
@@ -224,7 +239,8 @@ def swiglu_gate_up(x_flat: torch.Tensor, disp: Dispatch, w_in: torch.Tensor,
     rc = _lib.lib().mep_swiglu_gate_up(x.data_ptr(), n, disp.top_k, disp.perm.data_ptr(),
                                        disp.offsets.data_ptr(), disp.n_local, n * disp.top_k,
                                        wi.data_ptr(), h, inter, _dtype_code(x), act.data_ptr(),
-                                       act.numel() * act.element_size(), _stream(dev))
+                                       act.numel() * act.element_size(), _tile_queue(dev).data_ptr(),
+                                       _stream(dev))
     _lib.check(rc, "mep_swiglu_gate_up")
     return act
 
@@ -239,7 +255,8 @@ def swiglu_down(act: torch.Tensor, x_flat: torch.Tensor, disp: Dispatch, w_out: 
     wo = w_out.to(act.dtype).contiguous()
     rc = _lib.lib().mep_swiglu_down(act.data_ptr(), n, disp.top_k, disp.perm.data_ptr(),
                                     disp.offsets.data_ptr(), disp.n_local, n * disp.top_k, wo.data_ptr(),
-                                    h, inter, _dtype_code(act), y_entries.data_ptr(), _stream(dev))
+                                    h, inter, _dtype_code(act), y_entries.data_ptr(),
+                                    _tile_queue(dev).data_ptr(), _stream(dev))
     _lib.check(rc, "mep_swiglu_down")
     return y_entries
 

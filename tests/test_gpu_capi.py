@@ -42,8 +42,11 @@ def _moe_layer_raw(L, x, w_r, w_in, w_out, k=8):
     ok(L.mep_dispatch_check(ws.data_ptr(), s))
     act = torch.empty(L.mep_experts_workspace_size(N * k, I, BF16), dtype=torch.uint8, device="cuda")
     y = torch.empty(N * k, H, dtype=x.dtype, device="cuda")
+    queue = torch.zeros(2, dtype=torch.int32, device="cuda")
     ok(L.mep_grouped_swiglu(x.data_ptr(), N, k, perm.data_ptr(), offsets.data_ptr(), E, N * k, w_in.data_ptr(),
-                            w_out.data_ptr(), H, I, BF16, y.data_ptr(), act.data_ptr(), act.numel(), s))
+                            w_out.data_ptr(), H, I, BF16, y.data_ptr(), act.data_ptr(), act.numel(),
+                            queue.data_ptr(), s))
+    assert queue.tolist() == [0, 0]                      # every launch leaves the tile queue at zero
     out = torch.empty(N, H, dtype=x.dtype, device="cuda")
     ok(L.mep_combine(y.data_ptr(), gate.data_ptr(), row.data_ptr(), None, N, k, H, BF16, out.data_ptr(), s))
     return out, idx, gate
@@ -76,6 +79,6 @@ def test_error_codes_and_messages():
     rc = L.mep_combine(None, None, None, None, 4, 8, 1024, 1, None, None)
     assert rc == _lib.ERR_INVALID_ARG
     rc = L.mep_grouped_swiglu(x.data_ptr(), 4, 8, x.data_ptr(), x.data_ptr(), 4, 32, x.data_ptr(), x.data_ptr(),
-                              1024, 512, 1, x.data_ptr(), x.data_ptr(), 16, None)
+                              1024, 512, 1, x.data_ptr(), x.data_ptr(), 16, x.data_ptr(), None)
     assert rc == _lib.ERR_WORKSPACE
-    assert L.mep_abi_version() == 1
+    assert L.mep_abi_version() == 2

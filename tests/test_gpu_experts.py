@@ -120,3 +120,35 @@ def test_errors():
         ops.grouped_swiglu(x, d, torch.randn(3, 1024, 1024, device=DEV), torch.randn(3, 1024, 512, device=DEV))
     with pytest.raises(RuntimeError, match="inter"):
         ops.grouped_swiglu(x, d, torch.randn(4, 200, 1024, device=DEV), torch.randn(4, 1024, 100, device=DEV))
+
+
+def test_tile_queue_two_streams_and_repeats():
+    """The bf16 GEMMs hand out their last round of tiles through a per-stream
+    counter pair: launches on two streams at once and many launches in a row
+    give the serial result bit for bit, and leave every counter at zero."""
+    banner("experts tile queue")
+    outs = []
+    cases = []
+    for seed, T in ((3, 4096), (4, 3000)):
+        L = workloads.make_layer(T, seed=seed, zipf_s=1.2)
+        bf = torch.bfloat16
+        x = L.x.to(bf).to(DEV)
+        topk = (L.x @ L.w_router.T).topk(8, dim=-1).indices.to(DEV)
+        E = L.w_in.shape[0]
+        table, n_rep, g2l = _world1(E)
+        d = ops.dispatch(topk, None, E, table, n_rep, False, None, 0, g2l, E)
+        cases.append((x, d, L.w_in.to(bf).to(DEV), L.w_out.to(bf).to(DEV)))
+    ref = [ops.grouped_swiglu(*c) for c in cases]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    ys = [torch.empty_like(r) for r in ref]
+    torch.cuda.synchronize()
+    for _ in range(5):
+        for s, c, y in zip(streams, cases, ys):
+            with torch.cuda.stream(s):
+                ops.grouped_swiglu(*c, y)
+        torch.cuda.synchronize()
+        for y, r in zip(ys, ref):
+            assert torch.equal(y, r)
+    for q in ops._QUEUES.values():
+        assert q.tolist() == [0, 0]
