@@ -102,6 +102,81 @@ __global__ __launch_bounds__(kThreads) void combine_kernel(const typename Elem<D
   *reinterpret_cast<u32x4*>(out + t * hidden + c * EPC) = o;
 }
 
+// k = 8, (token, slot) layout: the 8 cells of a token, its row_of_entry
+// entries, gates and valid flag are independent loads, all issued together
+// (no LDS staging and no barrier before the first y load).  An absent cell is
+// skipped with a select, so whatever an unwritten cell holds never reaches the
+// sum, and the sum is the same slot-order sequence as in combine_kernel.
+template <int DT>
+__global__ __launch_bounds__(kThreads) void combine8_kernel(const typename Elem<DT>::T* __restrict__ y,
+                                                            const typename Elem<DT>::T* __restrict__ gate,
+                                                            const int32_t* __restrict__ row_of_entry,
+                                                            const uint8_t* __restrict__ valid,
+                                                            int64_t n_tokens, int hidden,
+                                                            typename Elem<DT>::T* __restrict__ out) {
+  typedef typename Elem<DT>::T T;
+  constexpr int K = 8;
+  constexpr int EPC = 16 / Elem<DT>::kBytes;
+  const int tpt = hidden / EPC;                         // threads per token
+  const int tokens_per_block = kThreads / tpt;
+  const int tid = threadIdx.x;
+  const int local_tok = tid / tpt;
+  const int c = tid - local_tok * tpt;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * tokens_per_block + local_tok;
+  if (local_tok >= tokens_per_block || t >= n_tokens) return;
+  const T* ybase = y + (t * K) * hidden + c * EPC;
+  u32x4 v[K];
+#pragma unroll
+  for (int s = 0; s < K; ++s) v[s] = *reinterpret_cast<const u32x4*>(ybase + static_cast<int64_t>(s) * hidden);
+  int32_t row[K];
+  float g[K];
+#pragma unroll
+  for (int s = 0; s < K; ++s) {
+    row[s] = row_of_entry[t * K + s];
+    g[s] = Elem<DT>::to_f32(gate[t * K + s]);
+  }
+  const bool tok_ok = valid == nullptr || valid[t] != 0;
+  float acc[EPC];
+#pragma unroll
+  for (int q = 0; q < EPC; ++q) acc[q] = 0.0f;
+#pragma unroll
+  for (int s = 0; s < K; ++s) {
+    const bool here = tok_ok && row[s] >= 0;
+    float yv[EPC];
+    if constexpr (DT == MEP_DTYPE_BF16) {
+      const uint32_t w[4] = {v[s].x, v[s].y, v[s].z, v[s].w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        yv[2 * q] = bf16_to_f32(static_cast<uint16_t>(w[q] & 0xffffu));
+        yv[2 * q + 1] = bf16_to_f32(static_cast<uint16_t>(w[q] >> 16));
+      }
+    } else {
+      yv[0] = __uint_as_float(v[s].x);
+      yv[1] = __uint_as_float(v[s].y);
+      yv[2] = __uint_as_float(v[s].z);
+      yv[3] = __uint_as_float(v[s].w);
+    }
+#pragma unroll
+    for (int q = 0; q < EPC; ++q) {
+      const float sum = acc[q] + g[s] * yv[q];
+      acc[q] = here ? sum : acc[q];
+    }
+  }
+  u32x4 o;
+  if constexpr (DT == MEP_DTYPE_BF16) {
+    o.x = pack_bf16x2(acc[0], acc[1]);
+    o.y = pack_bf16x2(acc[2], acc[3]);
+    o.z = pack_bf16x2(acc[4], acc[5]);
+    o.w = pack_bf16x2(acc[6], acc[7]);
+  } else {
+    o.x = __float_as_uint(acc[0]);
+    o.y = __float_as_uint(acc[1]);
+    o.z = __float_as_uint(acc[2]);
+    o.w = __float_as_uint(acc[3]);
+  }
+  *reinterpret_cast<u32x4*>(out + t * hidden + c * EPC) = o;
+}
+
 // out[i, :] = x[perm[i] / top_k, :] (and ids_out[i] = topk_flat[perm[i]]):
 // one thread per 16 bytes of an output row.
 template <int DT>
@@ -146,7 +221,16 @@ int combine_entry(const char* fn, const void* y, const void* topk_gate, const in
   const int tokens_per_block = kThreads / (hidden / epc);
   const dim3 grid(static_cast<unsigned>((n_tokens + tokens_per_block - 1) / tokens_per_block));
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (dtype == MEP_DTYPE_BF16)
+  if (!INDEXED && top_k == 8) {
+    if (dtype == MEP_DTYPE_BF16)
+      combine8_kernel<MEP_DTYPE_BF16><<<grid, kThreads, 0, s>>>(
+          static_cast<const uint16_t*>(y), static_cast<const uint16_t*>(topk_gate), row_of_entry, valid_mask,
+          n_tokens, hidden, static_cast<uint16_t*>(out));
+    else
+      combine8_kernel<MEP_DTYPE_F32><<<grid, kThreads, 0, s>>>(
+          static_cast<const float*>(y), static_cast<const float*>(topk_gate), row_of_entry, valid_mask,
+          n_tokens, hidden, static_cast<float*>(out));
+  } else if (dtype == MEP_DTYPE_BF16)
     combine_kernel<MEP_DTYPE_BF16, INDEXED><<<grid, kThreads, 0, s>>>(
         static_cast<const uint16_t*>(y), static_cast<const uint16_t*>(topk_gate), row_of_entry,
         valid_mask, n_tokens, top_k, hidden, static_cast<uint16_t*>(out));
