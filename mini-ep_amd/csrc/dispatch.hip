@@ -33,8 +33,8 @@
 namespace mep {
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kChunk = 1024;          // entries per block
+constexpr int kThreads = 512;
+constexpr int kChunk = 512;           // entries per block: one round of the block
 constexpr int kMaxSeg = 16;
 constexpr int kMaxExperts = 256;
 
