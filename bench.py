@@ -27,6 +27,8 @@ counter summary (``profiles/*hbm_traffic.md``: rocprofv3 FETCH_SIZE and
 WRITE_SIZE passes over this script, scaled by what the same counters read for
 the 256 MiB calibration copy this script issues before its warm-up), or null
 when that summary is absent.
+``c4_rank_share`` (outside the timed region): one rank's share of 4-way
+expert parallelism under the reference's balanced plan at T=8192, per rank.
 ``cpu_baseline`` times the numpy oracle on a bounded sample of the same
 workload on the host cores (and on one core).
 """
@@ -106,6 +108,50 @@ def cpu_baseline(layer, tokens: int, single_tokens: int, min_seconds: float = 10
                       f"{np_} passes in {dt:.1f} s",
             "single_thread": {"value": single_tokens * np1 / dt1, "unit": "tokens/s", "cores": 1,
                               "sample": f"first {single_tokens} tokens, 1 thread, {np1} passes in {dt1:.1f} s"}}
+
+
+def rank_share_detail(dev, steps: int) -> dict:
+    """One rank's share of 4-way expert parallelism at its real shape: the
+    reference's balanced plan (results/plan_balanced.json, kept as the test
+    fixture tests/golden/plan_balanced.json), layer 2 (8 owned + 2 replica
+    experts per rank), T=8192 Zipf(1.1)-routed bf16 tokens from 4 source
+    segments (round-robin counters zeroed, as after reset_rr).  Per rank:
+    dispatch in share mode + GEMM-1 + GEMM-2 on its local experts, HIP events
+    around `steps` back-to-back calls (GPU-bound: replaying the call from a
+    captured graph measured no faster).  A share of 12.7-20.1k rows is one to
+    two rounds of 256x256 tiles, so its time hardly depends on its rows."""
+    import torch
+
+    from miniep_amd import HipEPShareBackend, Placement, ops, workloads
+
+    plan = json.loads((ROOT / "tests/golden/plan_balanced.json").read_text())
+    pl = Placement.from_plan(plan, device=dev)
+    T, H, I, K = 8192, workloads.HIDDEN, workloads.INTER, workloads.TOP_K
+    lay = workloads.make_layer(T, seed=3, zipf_s=1.1)
+    bf = torch.bfloat16
+    x = lay.x.to(bf).to(dev)
+    idx, _ = ops.router_topk(x, lay.w_router.to(bf).to(dev), K)
+    seg = [T * s // 4 for s in range(5)]
+    y = torch.empty(T * K, H, dtype=bf, device=dev)
+    ranks = []
+    for r in range(pl.world):
+        ids = pl.experts_of_rank(r)[2]
+        be = HipEPShareBackend(2, pl, r, lay.w_in[ids].to(bf).to(dev), lay.w_out[ids].to(bf).to(dev), check=False)
+        for _ in range(20):
+            disp, _ = be.share(x, idx, seg_tokens=seg, y_entries=y)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(steps):
+            be.share(x, idx, seg_tokens=seg, y_entries=y)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        rows = int(disp.offsets[-1])
+        ranks.append({"rank": r, "local_experts": len(ids), "rows": rows, "ms": ms,
+                      "TFLOP/s": 6.0 * rows * H * I / (ms / 1e3) / 1e12})
+    return {"workload": "rank share of 4-way EP, plan_balanced layer 2, T=8192 Zipf(1.1), 4 sources, bf16",
+            "measures": "dispatch (share mode) + GEMM-1 + GEMM-2 per call, back to back", "ranks": ranks}
 
 
 def traffic_from_profile() -> dict | None:
@@ -257,6 +303,7 @@ def main(argv=None) -> int:
                      "traffic_source": traffic["source"] if traffic else None,
                      "flops_per_launch": flops_g1, "mean_launch_ms": g1_ms},
         "stages": detail,
+        "c4_rank_share": rank_share_detail(dev, args.steps),
     }
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(layer, min(args.cpu_sample_tokens, T),
