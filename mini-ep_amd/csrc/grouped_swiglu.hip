@@ -92,6 +92,28 @@ __device__ __forceinline__ float silu_f(float v) {
   return v * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-v * 1.4426950408889634f));
 }
 
+// pre[j] = sum over experts i < j of ceil(rows_i / ROWS) * mult, pre[nl] = the
+// total, with rows_i = off[i+1] - off[i] (off and pre in LDS).  One wave
+// (the caller's wave 0) scans 64 experts per pass with lane shuffles; the
+// caller synchronises the workgroup before and after.
+template <int ROWS>
+__device__ void scan_units(const int* off, int* pre, int nl, int mult) {
+  const int lane = threadIdx.x & 63;
+  int carry = 0;
+  for (int j0 = 0; j0 < nl; j0 += 64) {
+    const int j = j0 + lane;
+    int c = j < nl ? ((off[j + 1] - off[j] + ROWS - 1) / ROWS) * mult : 0;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int v = __shfl_up(c, d, 64);
+      if (lane >= d) c += v;
+    }
+    if (j < nl) pre[j + 1] = carry + c;
+    carry += __shfl(c, 63, 64);
+  }
+  if (lane == 0) pre[0] = 0;
+}
+
 constexpr int pow2_floor(int v) { int r = 1; while (r * 2 <= v) r *= 2; return r; }
 
 // Workgroup barrier that orders LDS only: this wave's LDS reads and writes
@@ -144,12 +166,7 @@ __global__ __launch_bounds__(Cfg::NT) void grouped_gemm_kernel(GemmParams p) {
   // ---- tile table: tiles per expert, prefix over experts ---------------------
   for (int j = tid; j <= nl; j += NT) s_off[j] = p.offsets[j];
   __syncthreads();
-  for (int j = tid; j < nl; j += NT)
-    s_prefix[j + 1] = ((s_off[j + 1] - s_off[j] + BM - 1) / BM) * p.n_tiles_n;
-  if (tid == 0) s_prefix[0] = 0;
-  __syncthreads();
-  if (tid == 0)
-    for (int j = 0; j < nl; ++j) s_prefix[j + 1] += s_prefix[j];
+  if (tid < 64) scan_units<BM>(s_off, s_prefix, nl, p.n_tiles_n);
   __syncthreads();
   const int total = __builtin_amdgcn_readfirstlane(s_prefix[nl]);
   const int per_xcd = (total + 7) / 8;
@@ -515,12 +532,7 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
   // ---- tile table ---------------------------------------------------------------
   for (int j = tid; j <= nl; j += NT) s_off[j] = p.offsets[j];
   __syncthreads();
-  for (int j = tid; j < nl; j += NT)
-    s_prefix[j + 1] = ((s_off[j + 1] - s_off[j] + BM - 1) / BM) * p.n_tiles_n;
-  if (tid == 0) s_prefix[0] = 0;
-  __syncthreads();
-  if (tid == 0)
-    for (int j = 0; j < nl; ++j) s_prefix[j + 1] += s_prefix[j];
+  if (tid < 64) scan_units<BM>(s_off, s_prefix, nl, p.n_tiles_n);
   __syncthreads();
   const int total = __builtin_amdgcn_readfirstlane(s_prefix[nl]);
   // Work items.  XCD x owns tiles [lo(x), hi(x)); its nslots workgroups take
@@ -925,6 +937,150 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
   }
 }
 
+// ============================================================================
+// bf16 path for few rows per expert (decode, small batches): one workgroup
+// per (chunk of at most 32 rows of one local expert, column block), 4 waves,
+// each wave two 16-column weight fragments (GEMM-1: 16 gate + the matching 16
+// up columns; GEMM-2: 32 output columns) against the chunk's two row
+// fragments.  There the time goes to streaming the weights from HBM, so each
+// wave keeps kSkinnyDepth K-steps of weight and row fragments in flight,
+// straight from global memory into VGPRs (no LDS, no barriers), and a
+// expert with no rows has no chunk, so its weights are never read.  K is walked in exactly
+// the main kernel's order (its column tile's rotation of the K stages, the
+// same MFMA with the weight fragment as src0), so every output element gets
+// the same fp32 accumulation sequence and the same bits as from
+// moe_gemm_bf16_kernel, whichever kernel the launch size selects.
+namespace skinny {
+constexpr int NW = 4, NT = NW * 64;
+constexpr int MFC = 2;                        // row fragments per pass (32 rows)
+constexpr int DEPTH = 8;                      // K-steps of loads in flight
+// use this path when N * k is at most this (measured crossover against the
+// tiled kernel: GEMM-1 between 1024 and 2048 entries, GEMM-2 past 2048)
+constexpr int64_t kMaxEntries1 = 1024, kMaxEntries2 = 2048;
+}  // namespace skinny
+
+template <bool GEMM1>
+__global__ __launch_bounds__(skinny::NT) void moe_gemm_skinny_kernel(GemmParams p) {
+  using namespace skinny;
+  typedef uint16_t T;
+  constexpr int CH = 16 * MFC;                                // rows per workgroup
+  __shared__ int s_pre[bfk::NLMAX + 1];                       // chunks before expert j
+  __shared__ int s_off[bfk::NLMAX + 1];
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nl = p.n_local;
+  // chunk table: expert j owns ceil(rows_j / CH) chunks of CH rows; workgroup
+  // b takes chunk b / n_cb in column block b % n_cb (the grid is sized for
+  // the worst case; workgroups past the last chunk return)
+  for (int j = tid; j <= nl; j += NT) s_off[j] = p.offsets[j];
+  __syncthreads();
+  if (tid < 64) scan_units<CH>(s_off, s_pre, nl, 1);
+  __syncthreads();
+  const int n_cb = GEMM1 ? p.N / 64 : p.N / 128;             // column blocks per expert
+  const int q = blockIdx.x / n_cb, cb = blockIdx.x % n_cb;
+  if (q >= s_pre[nl]) return;
+  int lo = 0, hi = nl - 1;                                    // largest j with s_pre[j] <= q
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (s_pre[mid] <= q) lo = mid; else hi = mid - 1;
+  }
+  const int e = __builtin_amdgcn_readfirstlane(lo);
+  const int row_lo = __builtin_amdgcn_readfirstlane(s_off[e] + (q - s_pre[e]) * CH);
+  const int row_hi = __builtin_amdgcn_readfirstlane(min(s_off[e + 1], row_lo + CH));
+  const int lr = lane & 15, lg = lane >> 4;
+  const int K = p.K, KT = K / 32, KD = K / 64;
+  // the main kernel's column tile of this block and its K rotation (in steps)
+  const int nt = cb / 2;
+  const int rot = (KD % 4 == 0) ? 2 * (nt & 3) * (KD / 4) : 0;
+  // weight rows of this wave's two fragments
+  const T* W = static_cast<const T*>(p.W) + static_cast<int64_t>(e) * p.w_expert_stride;
+  int wrow[2];
+  if constexpr (GEMM1) {
+    const int g0 = cb * 64 + wave * 16;
+    wrow[0] = g0 + lr;                       // gate column
+    wrow[1] = p.N + g0 + lr;                 // its up column
+  } else {
+    const int c0 = cb * 128 + wave * 32;
+    wrow[0] = c0 + lr;
+    wrow[1] = c0 + 16 + lr;
+  }
+  const T* wp0 = W + static_cast<int64_t>(wrow[0]) * K + 8 * lg;
+  const T* wp1 = W + static_cast<int64_t>(wrow[1]) * K + 8 * lg;
+  const T* A = static_cast<const T*>(p.A);
+  T* const C = static_cast<T*>(p.C);
+
+  {
+    const int r0 = row_lo;
+    // A rows of the pass (rows past row_hi read the last row; never stored)
+    const T* ap[MFC];
+#pragma unroll
+    for (int f = 0; f < MFC; ++f) {
+      const int r = min(r0 + 16 * f + lr, row_hi - 1);
+      int64_t src;
+      if constexpr (GEMM1) src = p.perm[r] / p.top_k;      // token row of x
+      else src = r;                                        // act row
+      ap[f] = A + src * K + 8 * lg;
+    }
+    u32x4 wq[DEPTH][2], aq[DEPTH][MFC];
+    auto load = [&](int t, int slot) {
+      int ks = t + rot;
+      if (ks >= KT) ks -= KT;
+      const int64_t off = static_cast<int64_t>(ks) * 32;
+      wq[slot][0] = *reinterpret_cast<const u32x4*>(wp0 + off);
+      wq[slot][1] = *reinterpret_cast<const u32x4*>(wp1 + off);
+#pragma unroll
+      for (int f = 0; f < MFC; ++f) aq[slot][f] = *reinterpret_cast<const u32x4*>(ap[f] + off);
+    };
+    // accumulators start at +0.0, which is what the main kernel's first MFMA
+    // adds (C operand 0), so the sums are the same bit for bit
+    f32x4 acc[MFC][2];
+#pragma unroll
+    for (int f = 0; f < MFC; ++f)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) acc[f][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) load(d, d);
+    for (int t0 = 0; t0 < KT; t0 += DEPTH) {             // KT is a multiple of DEPTH
+#pragma unroll
+      for (int d = 0; d < DEPTH; ++d) {
+#pragma unroll
+        for (int f = 0; f < MFC; ++f)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) mfma_acc(acc[f][j], wq[d][j], aq[d][f]);
+        if (t0 + d + DEPTH < KT) load(t0 + d + DEPTH, d);
+      }
+    }
+    // results: lane (lr, lg) of fragment j holds columns 4 lg .. 4 lg + 3 of
+    // the fragment for row lr of each row fragment
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+#pragma unroll
+    for (int f = 0; f < MFC; ++f)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) pin_acc(acc[f][j]);
+#pragma unroll
+    for (int f = 0; f < MFC; ++f) {
+      const int r = r0 + 16 * f + lr;
+      if (r >= row_hi) continue;
+      if constexpr (GEMM1) {
+        const int col = cb * 64 + wave * 16 + 4 * lg;
+        uint32_t w[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          w[h] = pack_bf16x2(silu_f(acc[f][0][2 * h]) * acc[f][1][2 * h],
+                             silu_f(acc[f][0][2 * h + 1]) * acc[f][1][2 * h + 1]);
+        *reinterpret_cast<uint2*>(C + static_cast<int64_t>(r) * p.N + col) = make_uint2(w[0], w[1]);
+      } else {
+        const int64_t row = p.perm[r];                     // (token, slot) cell
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int col = cb * 128 + wave * 32 + 16 * j + 4 * lg;
+          const uint2 w = make_uint2(pack_bf16x2(acc[f][j][0], acc[f][j][1]), pack_bf16x2(acc[f][j][2], acc[f][j][3]));
+          *reinterpret_cast<uint2*>(C + row * p.N + col) = w;
+        }
+      }
+    }
+  }
+}
+
 template <bool GEMM1>
 hipError_t launch_bf16(const GemmParams& p, int64_t max_rows, hipStream_t stream) {
   static int n_cu = 0;
@@ -933,6 +1089,15 @@ hipError_t launch_bf16(const GemmParams& p, int64_t max_rows, hipStream_t stream
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n_cu <= 0)
       n_cu = 256;
+  }
+  if (max_rows <= (GEMM1 ? skinny::kMaxEntries1 : skinny::kMaxEntries2)) {
+    // few rows per expert: stream each expert's weights once (same results)
+    const int n_cb = GEMM1 ? p.N / 64 : p.N / 128;
+    const int64_t chunks = (max_rows + 16 * skinny::MFC - 1) / (16 * skinny::MFC) + p.n_local;
+    const int64_t blocks = chunks * n_cb;
+    if (blocks == 0) return hipSuccess;
+    moe_gemm_skinny_kernel<GEMM1><<<dim3(static_cast<unsigned>(blocks)), skinny::NT, 0, stream>>>(p);
+    return hipGetLastError();
   }
   int64_t tiles = ((max_rows + bfk::BM - 1) / bfk::BM + p.n_local) * p.n_tiles_n;
   if (tiles == 0) return hipSuccess;
