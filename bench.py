@@ -27,6 +27,10 @@ counter summary (``profiles/*hbm_traffic.md``: rocprofv3 FETCH_SIZE and
 WRITE_SIZE passes over this script, scaled by what the same counters read for
 the 256 MiB calibration copy this script issues before its warm-up), or null
 when that summary is absent.
+``grouped_gemm_mfma_util_pct`` is algorithmic GEMM flops over the GEMM stage
+times against the 2.5 PFLOP/s nameplate; ``mfma_busy_counters`` is the
+hardware's own view from the committed counter summary
+(``profiles/*mfma_busy*.md``: MFMA busy cycles over active cycles).
 ``c4_rank_share`` (outside the timed region): one rank's share of 4-way
 expert parallelism under the reference's balanced plan at T=8192, per rank.
 ``cpu_baseline`` times the numpy oracle on a bounded sample of the same
@@ -108,6 +112,17 @@ def cpu_baseline(layer, tokens: int, single_tokens: int, min_seconds: float = 10
                       f"{np_} passes in {dt:.1f} s",
             "single_thread": {"value": single_tokens * np1 / dt1, "unit": "tokens/s", "cores": 1,
                               "sample": f"first {single_tokens} tokens, 1 thread, {np1} passes in {dt1:.1f} s"}}
+
+
+def mfma_busy_from_profile() -> dict | None:
+    """MFMA busy / active cycles of the two GEMMs from the committed counter
+    summary (rocprofv3 SQ_VALU_MFMA_BUSY_CYCLES and GRBM_GUI_ACTIVE), if any."""
+    for f in sorted((ROOT / "profiles").glob("*mfma_busy*.md")):
+        m = re.search(r"mfma_busy_pct = gemm1 ([0-9.]+), gemm2 ([0-9.]+), both ([0-9.]+)", f.read_text())
+        if m:
+            return {"gemm1_pct": float(m.group(1)), "gemm2_pct": float(m.group(2)), "both_pct": float(m.group(3)),
+                    "source": f"profiles/{f.name}"}
+    return None
 
 
 def rank_share_detail(dev, steps: int) -> dict:
@@ -295,6 +310,7 @@ def main(argv=None) -> int:
         "config": {"workload": WORKLOAD, "tokens": T, "hidden": H, "experts": E, "top_k": K,
                    "inter": I, "entries": M, "hottest_over_mean": round(hottest, 3)},
         "grouped_gemm_mfma_util_pct": 100.0 * gemm_util,
+        "mfma_busy_counters": mfma_busy_from_profile(),
         "layer_tflops": (flops_g1 + flops_g2) / (ms_step / 1e3) / 1e12,
         "roofline": {"kernel": "moe_gemm_bf16_kernel<true> (GEMM-1: gate/up + SwiGLU)", "bound": "mfma",
                      "achieved": achieved, "peak": PEAK_BF16_FLOPS / 1e12, "unit": "TFLOP/s",
