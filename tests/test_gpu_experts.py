@@ -188,3 +188,27 @@ def test_small_batch_kernel_matches_main_kernel_bitwise(stride):
     ref = O.experts(xr[rows // 8], to_np(topk[sel]).reshape(-1), wi.float().cpu().numpy(),
                     wo.float().cpu().numpy(), act_bf16=True, out_bf16=True)
     assert rel_err(to_np(y_small), ref) <= TOL_BF16
+
+
+@pytest.mark.parametrize("H,I,E,k,n,dtype", [
+    (256, 128, 8, 2, 700, torch.bfloat16),      # K = 256 (no steady steps); GEMM-2 on the generic kernel (I % 256)
+    (512, 384, 16, 4, 600, torch.bfloat16),     # tiled GEMM-1, generic GEMM-2
+    (2048, 256, 8, 8, 100, torch.bfloat16),     # 800 entries: small-batch kernels, K = 2048 / 256
+    (768, 640, 12, 6, 1000, torch.bfloat16),    # 3 column tiles of GEMM-1, 5 of 128 gate columns
+    (512, 256, 16, 4, 2000, torch.bfloat16),    # tiled kernels for both GEMMs, K = 512 / 256
+    (256, 256, 8, 2, 300, torch.float32),       # fp32
+])
+def test_other_shapes_vs_oracle(H, I, E, k, n, dtype):
+    banner(f"experts shape H={H} I={I} E={E} k={k} n={n} {dtype}")
+    g = torch.Generator().manual_seed(H + I + E + k)
+    x = torch.randn(n, H, generator=g)
+    w_in, w_out = workloads.expert_weights(g, E, H, I)
+    topk = torch.rand(n, E, generator=g).topk(k, -1).indices
+    d, y = _run(x, topk, w_in, w_out, dtype)
+    bf = dtype == torch.bfloat16
+    xr = x.to(dtype).float().numpy()
+    ref = O.experts(xr[np.repeat(np.arange(n), k)], topk.numpy().reshape(-1), w_in.to(dtype).float().numpy(),
+                    w_out.to(dtype).float().numpy(), act_bf16=bf, out_bf16=bf)
+    err = rel_err(to_np(y), ref)
+    print(f"rel err {err:.3e}")
+    assert err <= (TOL_BF16 if bf else TOL_F32)
