@@ -132,3 +132,22 @@ def test_rank_share_rows_match_oracle(golden_dir):
     ref = O.experts(xr[rows // 8], eids, L.w_in[ids].to(torch.bfloat16).float().numpy(),
                     L.w_out[ids].to(torch.bfloat16).float().numpy(), act_bf16=True, out_bf16=True)
     assert rel_err(to_np(y)[rows], ref) <= TOL_BF16
+
+
+@pytest.mark.parametrize("H,I,E,k,n,dtype", [
+    (2048, 256, 64, 4, 300, torch.bfloat16),
+    (512, 384, 16, 2, 1000, torch.bfloat16),
+    (512, 256, 64, 6, 700, torch.float32),
+])
+def test_layer_other_shapes(H, I, E, k, n, dtype):
+    """Router (E = 16 / 64), dispatch, experts and combine at other shapes."""
+    banner(f"layer shape H={H} I={I} E={E} k={k} n={n} {dtype}")
+    L = workloads.make_layer(n, seed=E + k, zipf_s=1.1, hidden=H, n_experts=E, top_k=k, inter=I)
+    valid = torch.rand(n, generator=torch.Generator().manual_seed(7)) < 0.9
+    out, idx, gate, logits, _ = _layer_on_gpu(L, dtype, valid)
+    ref, ridx, _ = _oracle_layer(L, dtype, to_np(logits), valid)
+    assert np.array_equal(to_np(idx), ridx)
+    err = rel_err(to_np(out), ref)
+    print(f"rel err {err:.3e}")
+    assert err <= (TOL_BF16 if dtype == torch.bfloat16 else TOL_F32)
+    assert (to_np(out)[~valid.numpy()] == 0).all()
