@@ -449,11 +449,15 @@ hipError_t launch(const GemmParams& p, int64_t max_rows, hipStream_t stream) {
 // register files and spills).
 //
 // Epilogue straight from the accumulators (16-byte stores, see pair_cols;
-// GEMM-2 regroups them into whole lines in LDS), no workgroup barrier.  The K order of a tile is rotated by its column-tile
-// index (n_tile * KD / 4 stages), which spreads the tiles running at the same
-// time over more memory channels; the rotation depends only on the output
-// columns, so every output element is summed in the same order wherever its
-// row sits in the dispatch.
+// GEMM-2 regroups them into whole lines in LDS), no workgroup barrier.
+// GEMM-2 rotates the K order of a tile by its column-tile index (n_tile * KD /
+// 4 stages), which spreads the tiles running at the same time over more
+// memory channels.  GEMM-1 does not: its 4 column tiles of a row tile run
+// side by side on one XCD and then read the same gathered x rows at about the
+// same time, so 3 of the 4 reads hit that XCD's L2 (measured on one box: 234
+// -> 223 us without the rotation).  Either way the order depends only on the
+// output columns, so every output element is summed in the same order
+// wherever its row sits in the dispatch.
 namespace bfk {
 constexpr int BM = 256, BN = 256, NT = 512, NW = 8;
 constexpr int KS = 32;                        // K per MFMA step (16x16x32)
@@ -623,7 +627,7 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
     int wv = wave;                             // opaque here too: no per-block constant is hoisted
     asm volatile("" : "+s"(wv));
     Src s;
-    s.rot = (KD % 4 == 0) ? (t.nt & 3) * (KD / 4) : 0;
+    s.rot = (!GEMM1 && KD % 4 == 0) ? (t.nt & 3) * (KD / 4) : 0;
     if (wave_a) {
       s.base = static_cast<const unsigned char*>(p.A);
       s.bytes = static_cast<int>(p.a_bytes);
@@ -946,7 +950,7 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
 // wave keeps kSkinnyDepth K-steps of weight and row fragments in flight,
 // straight from global memory into VGPRs (no LDS, no barriers), and a
 // expert with no rows has no chunk, so its weights are never read.  K is walked in exactly
-// the main kernel's order (its column tile's rotation of the K stages, the
+// the main kernel's order (GEMM-2: its column tile's rotation of the K stages; the
 // same MFMA with the weight fragment as src0), so every output element gets
 // the same fp32 accumulation sequence and the same bits as from
 // moe_gemm_bf16_kernel, whichever kernel the launch size selects.
@@ -990,7 +994,7 @@ __global__ __launch_bounds__(skinny::NT) void moe_gemm_skinny_kernel(GemmParams 
   const int K = p.K, KT = K / 32, KD = K / 64;
   // the main kernel's column tile of this block and its K rotation (in steps)
   const int nt = cb / 2;
-  const int rot = (KD % 4 == 0) ? 2 * (nt & 3) * (KD / 4) : 0;
+  const int rot = (!GEMM1 && KD % 4 == 0) ? 2 * (nt & 3) * (KD / 4) : 0;
   // weight rows of this wave's two fragments
   const T* W = static_cast<const T*>(p.W) + static_cast<int64_t>(e) * p.w_expert_stride;
   int wrow[2];
