@@ -72,7 +72,7 @@ __global__ __launch_bounds__(kThreads) void combine_kernel(const typename Elem<D
     const T* ycell;
     if constexpr (INDEXED) ycell = y + static_cast<int64_t>(s_row[local_tok * k + s]) * hidden + c * EPC;
     else ycell = ybase + static_cast<int64_t>(s) * hidden;
-    const u32x4 v = *reinterpret_cast<const u32x4*>(ycell);
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(ycell));   // read once
     if constexpr (DT == MEP_DTYPE_BF16) {
       const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
@@ -127,7 +127,10 @@ __global__ __launch_bounds__(kThreads) void combine8_kernel(const typename Elem<
   const T* ybase = y + (t * K) * hidden + c * EPC;
   u32x4 v[K];
 #pragma unroll
-  for (int s = 0; s < K; ++s) v[s] = *reinterpret_cast<const u32x4*>(ybase + static_cast<int64_t>(s) * hidden);
+  // y is read exactly once: non-temporal loads keep these 268 MB (T=16384)
+  // from evicting x and the weights from the 256 MB MALL before the next layer
+  for (int s = 0; s < K; ++s)
+    v[s] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(ybase + static_cast<int64_t>(s) * hidden));
   int32_t row[K];
   float g[K];
 #pragma unroll
