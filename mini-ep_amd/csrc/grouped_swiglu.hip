@@ -831,9 +831,12 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
             const u32x4 v = *reinterpret_cast<const u32x4*>(stg + rr * 256 + ((lchunk ^ rr) << 4));
             const int r = wm * 64 + i * 16 + 8 * half + rr;
             const int64_t row = s_rows[parity * BM + r];                     // (token, slot) cell
-            // (non-temporal stores for the y rows were measured slower over
-            // the whole layer: the combine then reads them from HBM)
-            if (t.row0 + r < t.valid_end) *reinterpret_cast<u32x4*>(C + row * p.N + col0 + lchunk * 8) = v;
+            // non-temporal: y (N*k rows, 268 MB at T=16384) is larger than
+            // the MALL and read once by the combine (non-temporal loads as
+            // well); kept out of it, it no longer evicts act, x and the
+            // weights, which this and the next layer step read again
+            if (t.row0 + r < t.valid_end)
+              __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(C + row * p.N + col0 + lchunk * 8));
           }
           asm volatile("" ::: "memory");
         }
