@@ -136,7 +136,6 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(DispatchParams p) {
   __shared__ int keptbase[kMaxExperts];           // kept entries of e in earlier segments
   __shared__ int loff[kMaxExperts];               // first row of e's local expert
   __shared__ int lcount[kMaxExperts];             // rows per local expert
-  __shared__ int run[kMaxExperts];                // entries of e seen in earlier rounds
   __shared__ int wcnt[kThreads / 64][kMaxExperts + 1];
   __shared__ uint32_t flag;
 
@@ -145,9 +144,21 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(DispatchParams p) {
   const int s = segment_of_block(p, b);
   int64_t f0, f1;
   block_range(p, b, s, f0, f1);
+  // this thread's entry (a block is one round of entries), loaded first so
+  // that its latency overlaps the histogram pass below
+  static_assert(kChunk == kThreads, "one entry per thread");
+  const int64_t f = f0 + tid;
+  int key = E;                                    // E: no expert (padding, masked or out of range)
+  bool dropped = false;
+  if (f < f1) {
+    const bool valid = p.valid == nullptr || p.valid[f / p.k] != 0;
+    const int64_t e = p.topk_idx[f];
+    if (valid && e >= 0 && e < E) key = static_cast<int>(e);
+    else dropped = true;
+  }
 
   for (int i = tid; i < p.n_seg * kMaxExperts; i += kThreads) segtot[i / kMaxExperts][i % kMaxExperts] = 0;
-  for (int e = tid; e < E; e += kThreads) { pre[e] = 0; run[e] = 0; lcount[e] = 0; }
+  for (int e = tid; e < E; e += kThreads) { pre[e] = 0; lcount[e] = 0; }
   for (int i = tid; i < (kThreads / 64) * (kMaxExperts + 1); i += kThreads)
     wcnt[i / (kMaxExperts + 1)][i % (kMaxExperts + 1)] = 0;
   if (tid == 0) flag = 0;
@@ -230,60 +241,43 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(DispatchParams p) {
   const int lane = tid & 63, wave = tid >> 6;
   const int nbits = 32 - __clz(E);
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  for (int64_t base_f = f0; base_f < f1; base_f += kThreads) {
-    const int64_t f = base_f + tid;
-    int key = E;
-    if (f < f1) {
-      const int64_t t = f / p.k;
-      const bool valid = p.valid == nullptr || p.valid[t] != 0;
-      const int64_t e = p.topk_idx[f];
-      if (valid && e >= 0 && e < E) {
-        key = static_cast<int>(e);
-      } else {
-        p.row_of_entry[f] = -1;
-        if (p.dest != nullptr) p.dest[f] = -1;
-      }
-    }
-    uint64_t peers = ~0ull;
-    for (int bit = 0; bit < nbits; ++bit) {
-      const bool on = (key >> bit) & 1;
-      const uint64_t m = __ballot(on);
-      peers &= on ? m : ~m;
-    }
-    const int rank_w = __popcll(peers & lt_mask);
-    if (key < E && rank_w == 0) wcnt[wave][key] = __popcll(peers);
-    __syncthreads();
-    if (key < E) {
-      int w = pre[key] + run[key] + rank_w;
-      for (int ww = 0; ww < wave; ++ww) w += wcnt[ww][key];
-      const int e = key;
-      const int64_t rr0 = p.has_rep ? p.rr_snap[s * E + e] : 0;
-      const int R = reps(p, e);
-      // floor modulo, as torch's % on int64 tensors (ep.py:94)
-      const int slot = p.has_rep ? static_cast<int>(((rr0 + w) % R + R) % R) : 0;
-      const int d = p.table[e * p.rmax + slot];
-      if (p.dest != nullptr) p.dest[f] = d;
-      int row = -1;
-      if (d == p.my_rank) {
-        const int j = p.g2l[e];
-        if (j >= 0 && j < p.n_local) {
-          const int64_t kb = p.has_rep ? kept_before(p, e, w, rr0) : w;
-          row = loff[e] + keptbase[e] + static_cast<int>(kb);
-          p.perm[row] = static_cast<int32_t>(f);
-        } else {
-          atomicOr(&flag, kFlagResident);
-        }
-      }
-      p.row_of_entry[f] = row;
-    }
-    __syncthreads();
-    for (int e = tid; e < E; e += kThreads) {
-      int add = 0;
-      for (int ww = 0; ww < kThreads / 64; ++ww) { add += wcnt[ww][e]; wcnt[ww][e] = 0; }
-      run[e] += add;
-    }
-    __syncthreads();
+  if (dropped) {
+    p.row_of_entry[f] = -1;
+    if (p.dest != nullptr) p.dest[f] = -1;
   }
+  uint64_t peers = ~0ull;
+  for (int bit = 0; bit < nbits; ++bit) {
+    const bool on = (key >> bit) & 1;
+    const uint64_t m = __ballot(on);
+    peers &= on ? m : ~m;
+  }
+  const int rank_w = __popcll(peers & lt_mask);
+  if (key < E && rank_w == 0) wcnt[wave][key] = __popcll(peers);
+  __syncthreads();
+  if (key < E) {
+    int w = pre[key] + rank_w;
+    for (int ww = 0; ww < wave; ++ww) w += wcnt[ww][key];
+    const int e = key;
+    const int64_t rr0 = p.has_rep ? p.rr_snap[s * E + e] : 0;
+    const int R = reps(p, e);
+    // floor modulo, as torch's % on int64 tensors (ep.py:94)
+    const int slot = p.has_rep ? static_cast<int>(((rr0 + w) % R + R) % R) : 0;
+    const int d = p.table[e * p.rmax + slot];
+    if (p.dest != nullptr) p.dest[f] = d;
+    int row = -1;
+    if (d == p.my_rank) {
+      const int j = p.g2l[e];
+      if (j >= 0 && j < p.n_local) {
+        const int64_t kb = p.has_rep ? kept_before(p, e, w, rr0) : w;
+        row = loff[e] + keptbase[e] + static_cast<int>(kb);
+        p.perm[row] = static_cast<int32_t>(f);
+      } else {
+        atomicOr(&flag, kFlagResident);
+      }
+    }
+    p.row_of_entry[f] = row;
+  }
+  __syncthreads();
   if (tid == 0) p.flags[p.nbl + b] = flag;
 }
 
