@@ -114,9 +114,9 @@ __global__ __launch_bounds__(kThreads) void count_kernel(DispatchParams p) {
   int64_t f0, f1;
   block_range(p, b, s, f0, f1);
   for (int64_t f = f0 + tid; f < f1; f += kThreads) {
-    const int64_t t = f / p.k;
-    if (p.valid != nullptr && p.valid[t] == 0) continue;
+    // both loads issued together (f is in bounds whether or not the token is masked)
     const int64_t e = p.topk_idx[f];
+    if (p.valid != nullptr && p.valid[f / p.k] == 0) continue;
     if (e < 0 || e >= p.E) { atomicOr(&flag, kFlagRange); continue; }
     atomicAdd(&cnt[e], 1);
   }
