@@ -731,7 +731,14 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
           fb[j] = *reinterpret_cast<const u32x4*>(R + b_base[RKK] + b_off(j));
         }
         asm volatile("" ::: "memory");
+        // a wave two groups into its step goes ahead of the other wave of
+        // its SIMD until the step ends: the pair drifts apart instead of
+        // issuing its DMA blocks and fragment reads in lockstep (same box:
+        // GEMM-1 -1.6 us, GEMM-2 -2 us; raised from the first group, or
+        // later, it gains less)
+        if (j == 1) __builtin_amdgcn_s_setprio(1);
       }
+      __builtin_amdgcn_s_setprio(0);
     }
     if constexpr (!ODD) {
       // the stage DMA'd during the previous step has landed (nothing else this
