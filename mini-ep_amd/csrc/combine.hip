@@ -126,9 +126,9 @@ __global__ __launch_bounds__(kThreads) void combine8_kernel(const typename Elem<
   if (local_tok >= tokens_per_block || t >= n_tokens) return;
   const T* ybase = y + (t * K) * hidden + c * EPC;
   u32x4 v[K];
-#pragma unroll
   // y is read exactly once: non-temporal loads keep these 268 MB (T=16384)
   // from evicting x and the weights from the 256 MB MALL before the next layer
+#pragma unroll
   for (int s = 0; s < K; ++s)
     v[s] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(ybase + static_cast<int64_t>(s) * hidden));
   int32_t row[K];
