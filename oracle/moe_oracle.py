@@ -2,7 +2,8 @@
 
 TEST INFRASTRUCTURE, NOT PRODUCT CODE.  Only ``tests/``, ``__graft_entry__.smoke()``
 and the ``cpu_baseline`` leg of ``bench.py`` may import this module, and only
-as the checker / the timed CPU baseline.  The HIP path never calls into it.
+to compute expected results or the timed CPU baseline.  The HIP path never
+calls into it.
 
 Each function restates one piece of the reference algorithm (mini-EP,
 ``miniep/modeling.py`` and ``miniep/ep.py``) in plain numpy so that the GPU
