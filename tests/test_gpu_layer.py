@@ -138,6 +138,10 @@ def test_rank_share_rows_match_oracle(golden_dir):
     (2048, 256, 64, 4, 300, torch.bfloat16),
     (512, 384, 16, 2, 1000, torch.bfloat16),
     (512, 256, 64, 6, 700, torch.float32),
+    (256, 128, 16, 1, 1, torch.bfloat16),       # one token, k = 1, I not a multiple of 256
+    (256, 256, 16, 1, 37, torch.float32),
+    (1024, 512, 32, 8, 1, torch.bfloat16),      # one token through the small-batch kernels
+    (1024, 512, 64, 8, 3000, torch.bfloat16),   # 64 experts, tiled kernels
 ])
 def test_layer_other_shapes(H, I, E, k, n, dtype):
     """Router (E = 16 / 64), dispatch, experts and combine at other shapes."""
