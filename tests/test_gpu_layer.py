@@ -92,6 +92,27 @@ def test_skewed_bf16_t16384():
     assert torch.equal(out, out2)
 
 
+def test_largest_bf16_t262144():
+    """2^18 tokens: act is 2 GiB and y_entries 4 GiB, the sizes where the
+    kernels' 32-bit DMA offsets and int32 entry ids are closest to their
+    limits.  Routing bit-exact, counts equal the bincount, the first, last
+    and 512 random tokens against the oracle."""
+    banner("layer bf16 t=262144")
+    T = 262144
+    L = workloads.make_layer(T, seed=3, zipf_s=1.2)
+    out, idx, gate, logits, be = _layer_on_gpu(L, torch.bfloat16, check=False)
+    lg = to_np(logits)
+    ridx, _ = O.topk_softmax(lg, 8, gate_bf16=True)
+    assert np.array_equal(to_np(idx), ridx)
+    assert to_np(be.last_dispatch.counts).tolist() == np.bincount(ridx.reshape(-1), minlength=32).tolist()
+    toks = np.concatenate([np.arange(256), np.arange(T - 256, T),
+                           np.random.default_rng(1).choice(T, 512, replace=False)])
+    ref, _, _ = _oracle_layer(L, torch.bfloat16, lg, tokens=toks)
+    err = rel_err(to_np(out[torch.from_numpy(toks).to(DEV)]), ref)
+    print(f"rel err {err:.3e}")
+    assert err <= TOL_BF16
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_emulated_ep_equals_local_bitwise(golden_dir, dtype):
     """Placement invariance (ep.py:1-8): world-4 balanced plan, 4 sources, every
