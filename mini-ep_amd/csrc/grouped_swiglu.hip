@@ -12,25 +12,31 @@
 //   GEMM-2  y_entries[perm[r], :] = act[r, :] W_out^T
 //           rows are scattered straight to their (token, slot) cell.
 //
-// Tiling: BM x BN output tile, 8 waves (4 x 2) of 64 x 128.  K is staged 128
-// bytes per row at a time (64 bf16 / 32 fp32) through two LDS stages filled by
-// global_load_lds_dwordx4 (global memory straight into LDS, no VGPR staging):
-// one instruction moves 8 rows x 128 B; lane L lands at byte 16 L, so it
-// fetches logical chunk (L%8) ^ (L/8) of its row, which stores each row's
-// chunks XOR-swizzled by (row & 7) and makes the fragment reads (16 rows x one
-// chunk) bank-conflict free.  The MFMA takes the weight fragment as its first
-// operand, so it produces C^T: each lane holds 4 consecutive output columns of
-// one row, and the epilogue packs them into 8-byte LDS writes.
-// MFMA: v_mfma_f32_16x16x32_bf16 (bf16) or 4 x v_mfma_f32_16x16x4_f32 per
-// 16-byte chunk (fp32); accumulation is fp32 in both cases.
+// Tiling (bf16, moe_gemm_bf16_kernel): 256 x 256 output tile, 8 waves (4 x 2)
+// of 64 x 128.  K is staged 128 bytes per row at a time (64 bf16) through two
+// LDS stages filled by buffer_load ... lds (global memory straight into LDS,
+// no VGPR staging): one instruction moves 8 rows x 128 B; lane L lands at
+// byte 16 L, so it fetches logical chunk (L%8) ^ (L/8) of its row, which
+// stores each row's chunks XOR-swizzled by (row & 7) and makes the fragment
+// reads (16 rows x one chunk) bank-conflict free.  The MFMA
+// (v_mfma_f32_16x16x32_bf16, fp32 accumulation in VGPRs) takes the weight
+// fragment as its first operand, so it produces C^T; with the weight rows
+// permuted per 32-column group a lane ends up holding 8 consecutive output
+// columns of one row.  GEMM-1 applies SiLU * up in registers and stores 16 B
+// per lane; GEMM-2 regroups rows through a per-wave LDS slice into whole
+// 128-byte lines and stores them non-temporally (y_entries is read once, by
+// the combine).  fp32 keeps the simpler two-stage grouped_gemm_kernel.
 //
-// Scheduling: persistent.  One workgroup per CU walks a list of tiles
-// (expert, m-tile, n-tile) derived on the device from `offsets` (no host round
-// trip for the counts).  Workgroups are dealt to the 8 XCDs round-robin, so
-// workgroup b takes tiles (b mod 8) * ceil(T/8) + b/8 + i * (grid/8): the CUs
-// of one XCD sweep one contiguous run of tiles and share weights and rows in
-// their L2.  While a tile's epilogue drains through one LDS stage, the next
-// tile's first K step is already streaming into the other.
+// Scheduling (bf16): persistent, one workgroup per CU.  The tile list
+// (expert, m-tile, n-tile) is derived on the device from `offsets` (no host
+// round trip for the counts).  XCD x owns a contiguous run of tiles, and its
+// workgroups take them in whole rounds (the 4 column tiles of a row tile sit
+// on the same 4 slots of one XCD, so they share rows and weights in its L2);
+// the tiles left after the whole rounds form one pool that workgroups take
+// through an atomic counter in the caller's tile queue.  The next tile's first
+// two stages stream in during the last four steps and the epilogue of the
+// current one.  Within a step, a wave two MFMA groups in runs at raised
+// priority, which keeps the two waves of a SIMD from moving in lockstep.
 #include "common.h"
 
 #include <type_traits>
