@@ -21,10 +21,14 @@
 // c = (j - rr) mod R.  No atomics decide any position, so the permutation is
 // bit-identical to the reference's stable sorts on every run.
 //
-// Two launches over blocks of kChunk consecutive entries of one segment:
+// Launches over blocks of kChunk consecutive entries of one segment:
 //   count_kernel    per-block per-expert histogram (LDS atomics; counts only)
-//   scatter_kernel  every block re-derives the prefix of its segment and the
-//                   segment totals from the histograms (nb x E ints from L2),
+//   prefix_kernel   only above kScanBlocks blocks: one workgroup per expert
+//                   turns its histogram column into per-segment exclusive
+//                   prefixes and segment totals
+//   scatter_kernel  every block takes the prefix of its segment and the
+//                   segment totals (from prefix_kernel, or, for few blocks,
+//                   re-derived from the histograms: nb x E ints from L2),
 //                   then ranks its entries in flat order with wave ballots and
 //                   writes perm / row_of_entry / dest.  Block 0 also writes
 //                   counts, offsets, route_counts and the updated rr.
@@ -37,6 +41,9 @@ constexpr int kThreads = 512;
 constexpr int kChunk = 512;           // entries per block: one round of the block
 constexpr int kMaxSeg = 16;
 constexpr int kMaxExperts = 256;
+// above this many blocks the histograms are scanned once by prefix_kernel
+// instead of being summed again by every scatter block (nb^2 * E reads)
+constexpr int kScanBlocks = 512;
 
 struct DispatchParams {
   const int64_t* topk_idx;
@@ -61,6 +68,8 @@ struct DispatchParams {
   uint32_t* flags;      // [2 * nbl]: count-kernel flags, scatter-kernel flags
   int64_t* rr_snap;     // [S * E]
   int32_t* bc;          // [nbl * E]
+  int32_t* segtot;      // [n_seg * E], written by prefix_kernel
+  int scanned;          // 1: prefix_kernel turned bc into per-segment exclusive prefixes
   int nb, nbl, n_seg;
   int64_t seg_entry[kMaxSeg + 1];
   int seg_block[kMaxSeg + 1];
@@ -130,6 +139,56 @@ __global__ __launch_bounds__(kThreads) void count_kernel(DispatchParams p) {
   }
 }
 
+// One workgroup per expert e: within each source segment, replace the
+// column bc[b][e] by its exclusive prefix over the segment's blocks and write
+// the segment total to segtot[s][e] -- the same sums the scatter blocks would
+// otherwise each rebuild from the whole table.
+constexpr int kScanThreads = 256;
+__global__ __launch_bounds__(kScanThreads) void prefix_kernel(DispatchParams p) {
+  constexpr int V = 8;                                  // blocks per thread per pass
+  constexpr int NW = kScanThreads / 64;
+  __shared__ int wsum[NW];
+  const int e = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int s = 0; s < p.n_seg; ++s) {
+    const int b0 = p.seg_block[s], b1 = p.seg_block[s + 1];
+    int carry = 0;
+    for (int c0 = b0; c0 < b1; c0 += kScanThreads * V) {
+      int v[V];
+      int sum = 0;
+#pragma unroll
+      for (int u = 0; u < V; ++u) {
+        const int b = c0 + tid * V + u;
+        v[u] = b < b1 ? p.bc[static_cast<int64_t>(b) * p.E + e] : 0;
+        sum += v[u];
+      }
+      int x = sum;                                      // inclusive scan over the wave
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const int y = __shfl_up(x, d, 64);
+        if (lane >= d) x += y;
+      }
+      if (lane == 63) wsum[wave] = x;
+      __syncthreads();
+      int before = 0, total = 0;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        if (w < wave) before += wsum[w];
+        total += wsum[w];
+      }
+      int run = carry + before + x - sum;               // prefix of this thread's first block
+#pragma unroll
+      for (int u = 0; u < V; ++u) {
+        const int b = c0 + tid * V + u;
+        if (b < b1) p.bc[static_cast<int64_t>(b) * p.E + e] = run;
+        run += v[u];
+      }
+      carry += total;
+      __syncthreads();                                  // wsum is rewritten by the next pass
+    }
+    if (tid == 0) p.segtot[s * p.E + e] = carry;
+  }
+}
+
 __global__ __launch_bounds__(kThreads) void scatter_kernel(DispatchParams p) {
   __shared__ int segtot[kMaxSeg][kMaxExperts];   // entries of expert e in segment s
   __shared__ int pre[kMaxExperts];                // ... in earlier blocks of my segment
@@ -164,11 +223,15 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(DispatchParams p) {
   if (tid == 0) flag = 0;
   __syncthreads();
 
-  // 1. segment totals and my prefix, from the per-block histograms.  The
+  // 1. segment totals and my prefix: read from prefix_kernel's results, or
+  // summed here from the per-block histograms.  The
   // histogram loads of a thread are issued 8 at a time before any of them is
   // used (one L2 round trip per 8 blocks instead of one per block); with one
   // segment the total is summed in a register and added to LDS once.
-  {
+  if (p.scanned) {
+    for (int i = tid; i < p.n_seg * E; i += kThreads) segtot[i / E][i % E] = p.segtot[i];
+    for (int e = tid; e < E; e += kThreads) pre[e] = b < p.nb ? p.bc[static_cast<int64_t>(b) * E + e] : 0;
+  } else {
     const int parts = kThreads / E > 0 ? kThreads / E : 1;
     const int e = tid % E, part = tid / E;
     if (part < parts && tid < parts * E) {
@@ -284,7 +347,7 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(DispatchParams p) {
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 struct WsLayout {
-  size_t header, flags, rr_snap, bc, total;
+  size_t header, flags, rr_snap, bc, segtot, total;
 };
 
 WsLayout ws_layout(int nbl, int n_seg, int E) {
@@ -293,7 +356,8 @@ WsLayout ws_layout(int nbl, int n_seg, int E) {
   l.flags = 256;
   l.rr_snap = align_up(l.flags + sizeof(uint32_t) * 2 * nbl, 256);
   l.bc = align_up(l.rr_snap + sizeof(int64_t) * n_seg * E, 256);
-  l.total = align_up(l.bc + sizeof(int32_t) * static_cast<size_t>(nbl) * E, 256);
+  l.segtot = align_up(l.bc + sizeof(int32_t) * static_cast<size_t>(nbl) * E, 256);
+  l.total = align_up(l.segtot + sizeof(int32_t) * static_cast<size_t>(n_seg) * E, 256);
   return l;
 }
 
@@ -372,6 +436,8 @@ extern "C" int mep_dispatch(const int64_t* topk_idx, const uint8_t* valid_mask, 
   p.flags = reinterpret_cast<uint32_t*>(ws + l.flags);
   p.rr_snap = reinterpret_cast<int64_t*>(ws + l.rr_snap);
   p.bc = reinterpret_cast<int32_t*>(ws + l.bc);
+  p.segtot = reinterpret_cast<int32_t*>(ws + l.segtot);
+  p.scanned = p.nb > kScanBlocks ? 1 : 0;
   p.n_seg = n_segments;
   for (int s = 0; s <= n_segments; ++s) p.seg_entry[s] = seg_tokens[s] * top_k;
   for (int s = n_segments + 1; s <= kMaxSeg; ++s) { p.seg_entry[s] = p.seg_entry[n_segments]; p.seg_block[s] = p.nb; }
@@ -379,6 +445,10 @@ extern "C" int mep_dispatch(const int64_t* topk_idx, const uint8_t* valid_mask, 
   hipStream_t st = static_cast<hipStream_t>(stream);
   count_kernel<<<p.nbl, kThreads, 0, st>>>(p);
   MEP_CHECK_LAUNCH("mep_dispatch(count)");
+  if (p.scanned) {
+    prefix_kernel<<<n_experts, kScanThreads, 0, st>>>(p);
+    MEP_CHECK_LAUNCH("mep_dispatch(prefix)");
+  }
   scatter_kernel<<<p.nbl, kThreads, 0, st>>>(p);
   MEP_CHECK_LAUNCH("mep_dispatch(scatter)");
   return MEP_OK;

@@ -43,7 +43,8 @@ def _check(d, ref, n, k, n_local):
 
 @pytest.mark.parametrize("n,k,E,masked,zipf", [(3000, 8, 32, True, False), (16384, 8, 32, False, True),
                                                (1, 8, 32, False, False), (999, 3, 7, True, False),
-                                               (5000, 1, 256, False, False), (2048, 32, 64, True, True)])
+                                               (5000, 1, 256, False, False), (2048, 32, 64, True, True),
+                                               (70000, 8, 32, True, True)])   # > 512 blocks: scanned histograms
 def test_world1_grouping(n, k, E, masked, zipf):
     banner(f"dispatch world1 n={n} k={k} E={E}")
     topk = _routing(n, k, E, n + k, zipf)
@@ -84,16 +85,17 @@ def test_dest_ranks_every_plan_layer(golden_dir):
     assert int(p._rr.abs().sum()) == 0
 
 
-@pytest.mark.parametrize("sources", [1, 4])
-def test_rank_share_plan_layer2(golden_dir, sources):
+@pytest.mark.parametrize("sources,n", [(1, 8192), (4, 8192), (4, 40000)])
+def test_rank_share_plan_layer2(golden_dir, sources, n):
     """One rank's share under the reference's balanced plan, layer 2 (8 owned +
-    2 replicas per rank), T=8192 Zipf(1.1)-routed tokens from `sources` senders."""
-    banner(f"rank share layer2 sources={sources}")
+    2 replicas per rank), n Zipf(1.1)-routed tokens from `sources` senders
+    (n = 40000: 625 blocks, above the threshold for the scanned histograms)."""
+    banner(f"rank share layer2 sources={sources} n={n}")
     plan = json.loads((golden_dir / "plan_balanced.json").read_text())
     p = Placement.from_plan(plan, device=DEV)
-    L = workloads.make_layer(8192, seed=3, zipf_s=1.1)
+    L = workloads.make_layer(n, seed=3, zipf_s=1.1)
     topk = (L.x @ L.w_router.T).topk(8, dim=-1).indices
-    n, k, E = 8192, 8, 32
+    k, E = 8, 32
     seg = [n * s // sources for s in range(sources + 1)]
     table, n_rep = p.tables(2)
     t_ref, n_ref = O.build_table(p.owners[2])
