@@ -119,6 +119,48 @@ def test_rank_share_plan_layer2(golden_dir, sources, n):
     assert (seen == 1).all()          # the 4 shares partition the entries
 
 
+def test_random_placements_every_rank():
+    """Seeded random cases: experts with 1-3 owner ranks out of 4 (random
+    replica sets), 1-5 source segments of random sizes (empty ones included),
+    random masks and round-robin counters, every rank's share bit-exact against
+    the oracle, and the 4 shares partition the kept entries."""
+    rng = np.random.default_rng(11)
+    for case in range(12):
+        E = int(rng.choice([8, 16, 32, 64]))
+        k = int(rng.integers(1, min(E, 8) + 1))
+        n = int(rng.choice([1, 37, 513, 4000, 70000 if case == 11 else 9000]))
+        sources = int(rng.integers(1, 6))
+        banner(f"random placement case {case}: n={n} k={k} E={E} sources={sources}")
+        owners = [sorted(rng.choice(4, int(rng.integers(1, 4)), replace=False).tolist()) for _ in range(E)]
+        for r in range(4):                      # every rank owns at least one expert
+            if not any(r in o for o in owners):
+                e = int(rng.integers(E))
+                owners[e] = sorted(set(owners[e]) | {r})
+        p = Placement([owners], device=DEV)
+        table, n_rep = p.tables(0)
+        t_ref, n_ref = O.build_table(owners)
+        cuts = np.sort(rng.integers(0, n + 1, sources - 1))
+        seg = [0, *cuts.tolist(), n]
+        topk = torch.from_numpy(np.stack([rng.permutation(E)[:k] for _ in range(n)]).astype(np.int64))
+        valid = torch.from_numpy(rng.random(n) < 0.85)
+        rr0 = rng.integers(0, 5, (sources, E))
+        seen = np.zeros(n * k, np.int64)
+        for r in range(4):
+            local = p.experts_of_rank(r)[0]
+            g2l = np.full(E, -1)
+            g2l[local] = np.arange(len(local))
+            rr = torch.from_numpy(rr0.copy()).to(DEV)
+            d = ops.dispatch(topk.to(DEV), valid.to(DEV), E, table, n_rep, True, rr, r,
+                             torch.from_numpy(g2l).int().to(DEV), len(local), seg_tokens=seg, want_dest=True)
+            ref = O.dispatch(topk.numpy(), valid.numpy(), E, t_ref, n_ref, rr0, seg, r, g2l)
+            _check(d, ref, n, k, len(local))
+            assert to_np(d.dest).tolist() == ref["dest"].tolist()
+            assert to_np(rr).tolist() == ref["rr_after"].tolist()
+            seen[ref["perm"]] += 1
+        kept = np.repeat(valid.numpy(), k)
+        assert (seen[kept] == 1).all() and (seen[~kept] == 0).all()
+
+
 def test_empty_and_all_masked():
     banner("dispatch empty")
     E = 32
