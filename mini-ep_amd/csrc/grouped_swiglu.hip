@@ -551,13 +551,23 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
   // then XCD 1's, ...) that workgroups take one at a time through an atomic
   // counter once their own rounds are done, so the last round goes to
   // whichever workgroups finish first instead of a fixed, possibly slow,
-  // subset.  Which workgroup computes a tile does not change its result.
+  // subset.  GEMM-2 also puts each XCD's last whole round in the pool: its
+  // tile times vary more with the expert (cold weights of small experts), and
+  // a static last round left some XCDs a tile behind the others (same box,
+  // three routings: GEMM-2 -5 to -7 us).  GEMM-1 keeps that round on its own
+  // XCD, where the 4 column tiles of a row tile share the gathered x rows in
+  // L2 (moved to the pool, they cost GEMM-1 up to 5 us).  Which workgroup
+  // computes a tile does not change its result.
+  constexpr int kPoolRounds = GEMM1 ? 0 : 1;     // whole rounds per XCD added to the pool
   const int per_xcd = (total + 7) / 8;
   const int xcd = blockIdx.x % 8, slot = blockIdx.x / 8, nslots = gridDim.x / 8;
   auto xcd_lo = [&](int x) { return min(total, x * per_xcd); };
-  auto xcd_rem = [&](int x) { return (min(total, x * per_xcd + per_xcd) - xcd_lo(x)) % nslots; };
+  auto xcd_own = [&](int x) {                    // whole rounds XCD x keeps
+    return max((min(total, x * per_xcd + per_xcd) - xcd_lo(x)) / nslots - kPoolRounds, 0);
+  };
+  auto xcd_rem = [&](int x) { return min(total, x * per_xcd + per_xcd) - xcd_lo(x) - xcd_own(x) * nslots; };
   const int x_lo = xcd_lo(xcd);
-  const int n_priv = (min(total, x_lo + per_xcd) - x_lo) / nslots;
+  const int n_priv = xcd_own(xcd);
   int pool_size = 0;
   for (int x = 0; x < 8; ++x) pool_size += xcd_rem(x);
   pool_size = __builtin_amdgcn_readfirstlane(pool_size);
