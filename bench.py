@@ -183,7 +183,7 @@ def main(argv=None) -> int:
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}); "
-              "the multi-GPU expert-parallel path is design-only in this build", file=sys.stderr)
+              "the multi-GPU expert-parallel exchange (RCCL all-to-all) is not implemented; this library runs one GPU's share", file=sys.stderr)
         return 2
 
     import torch

@@ -15,7 +15,7 @@ Follows the reference model (miniep/modeling.py):
 Weights use the checkpoint's key names (weights.py:17-26), so a loaded
 checkpoint dict drops in.
 
-Choices of this build: the KV cache is preallocated per layer and written in
+Choices made here (not fixed by the reference): the KV cache is preallocated per layer and written in
 place (no concatenation per decode step); attention runs in fp32 (batched
 bf16 products with transposed operands are avoided on ROCm); the LM head is
 computed in fp32 for the positions asked for; router logits are fp32 (the
