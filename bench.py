@@ -31,10 +31,14 @@ when that summary is absent.
 times against the 2.5 PFLOP/s nameplate; ``mfma_busy_counters`` is the
 hardware's own view from the committed counter summary
 (``profiles/*mfma_busy*.md``: MFMA busy cycles over active cycles).
-``c4_rank_share`` (outside the timed region): one rank's share of 4-way
-expert parallelism under the reference's balanced plan at T=8192, per rank.
-``cpu_baseline`` times the numpy oracle on a bounded sample of the same
-workload on the host cores (and on one core).
+``c4_rank_share`` (measured before the warm-up, outside the timed region):
+one rank's share of 4-way expert parallelism under the reference's balanced
+plan at T=8192, per rank.  Order of the run: calibration copy, one routing
+pass, c4_rank_share, `warmup` steps, the `steps` timed steps, the per-stage
+pass, cpu_baseline.
+``cpu_baseline`` times the reference's algorithm restated in PyTorch-CPU
+(fp32) on the same workload on the host's CPU share (and on one core), with
+the numpy oracle's figure beside it.
 """
 from __future__ import annotations
 
@@ -66,52 +70,70 @@ def parse_args(argv=None):
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--tokens", type=int, default=16384)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-sample-tokens", type=int, default=16384)
     ap.add_argument("--cpu-single-thread-tokens", type=int, default=4096)
-    ap.add_argument("--cpu-seconds", type=float, default=10.0,
-                    help="minimum host time of the CPU baseline's multi-thread leg")
     return ap.parse_args(argv)
 
 
-def cpu_baseline(layer, tokens: int, single_tokens: int, min_seconds: float = 10.0) -> dict:
-    """The numpy oracle (router + LocalMoEBackend restatement, fp32) on the
-    first `tokens` tokens of the workload on the host cores (at most 16
-    threads), repeated for at least `min_seconds`, and on the first
-    `single_tokens` tokens on one thread for at least half that."""
+def cpu_baseline(layer, single_tokens: int, reps: int = 3) -> dict:
+    """The reference's algorithm on the host cores: the PyTorch-CPU
+    restatement of the router + LocalMoEBackend (oracle/torch_cpu.py, fp32, on
+    the bf16 values of the same workload), one warm-up pass, then the median
+    of `reps` passes over all tokens with the box's CPU share of threads (the
+    OMP_NUM_THREADS the box sets, at most the CPUs this process may run on),
+    and over the first `single_tokens` tokens on one thread (the reference's
+    own --threads 1 setting).  The numpy oracle's figure on the same threads
+    is reported beside it."""
     import numpy as np
     import torch
     from threadpoolctl import threadpool_limits
 
     from oracle import moe_oracle as O
+    from oracle import torch_cpu as TC
 
-    cores = max(1, min(len(os.sched_getaffinity(0)), 16))
-    x = layer.x.to(torch.bfloat16).float().numpy()
-    wr = layer.w_router.to(torch.bfloat16).float().numpy()
-    wi = layer.w_in.to(torch.bfloat16).float().numpy()
-    wo = layer.w_out.to(torch.bfloat16).float().numpy()
+    visible = len(os.sched_getaffinity(0))
+    threads = max(1, min(visible, int(os.environ.get("OMP_NUM_THREADS", visible) or visible)))
+    x = layer.x.to(torch.bfloat16).float()
+    wr = layer.w_router.to(torch.bfloat16).float()
+    wi = layer.w_in.to(torch.bfloat16).float()
+    wo = layer.w_out.to(torch.bfloat16).float()
+    T = x.shape[0]
 
-    def run(n: int, threads: int, min_s: float) -> tuple[float, int]:
-        """Repeat the layer on the first n tokens until at least min_s seconds
-        have passed; returns (seconds, passes)."""
-        passes, dt = 0, 0.0
-        with threadpool_limits(limits=threads):
-            while passes == 0 or dt < min_s:
-                t0 = time.perf_counter()
-                idx, gate = O.topk_softmax(O.router_logits(x[:n], wr), layer.top_k)
-                out = O.moe_layer_local(x[:n], idx, gate, wi, wo)
-                dt += time.perf_counter() - t0
-                passes += 1
-        assert np.isfinite(out).all()
-        return dt, passes
+    def median_seconds(fn) -> float:
+        fn()
+        times = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+        return float(np.median(times))
 
-    dt, np_ = run(tokens, cores, min_seconds)
-    dt1, np1 = run(single_tokens, 1, min_seconds / 2)
-    return {"value": tokens * np_ / dt, "unit": "tokens/s", "cores": cores, "kind": "port",
-            "sample": f"first {tokens} of the {layer.x.shape[0]} tokens, fp32 numpy oracle "
-                      f"(router + LocalMoEBackend restatement), {cores} threads, "
-                      f"{np_} passes in {dt:.1f} s",
-            "single_thread": {"value": single_tokens * np1 / dt1, "unit": "tokens/s", "cores": 1,
-                              "sample": f"first {single_tokens} tokens, 1 thread, {np1} passes in {dt1:.1f} s"}}
+    prev = torch.get_num_threads()
+    try:
+        torch.set_num_threads(threads)
+        with torch.no_grad():
+            t_all = median_seconds(lambda: TC.moe_block(x, wr, wi, wo, layer.top_k))
+        torch.set_num_threads(1)
+        n1 = min(single_tokens, T)
+        with torch.no_grad():
+            t_one = median_seconds(lambda: TC.moe_block(x[:n1], wr, wi, wo, layer.top_k))
+    finally:
+        torch.set_num_threads(prev)
+    xn, wrn, win, won = x.numpy(), wr.numpy(), wi.numpy(), wo.numpy()
+
+    def numpy_layer():
+        idx, gate = O.topk_softmax(O.router_logits(xn, wrn), layer.top_k)
+        O.moe_layer_local(xn, idx, gate, win, won)
+
+    with threadpool_limits(limits=threads):
+        t_np = median_seconds(numpy_layer)
+    return {"value": T / t_all, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"all {T} tokens of the workload, PyTorch-CPU restatement of the reference's router + "
+                      f"LocalMoEBackend (fp32), {threads} threads ({visible} CPUs visible to the process), "
+                      f"median of {reps} passes after 1 warm-up: {t_all:.3f} s per pass",
+            "single_thread": {"value": n1 / t_one, "unit": "tokens/s", "cores": 1,
+                              "sample": f"first {n1} tokens, 1 thread, median of {reps}: {t_one:.3f} s"},
+            "numpy_oracle": {"value": T / t_np, "unit": "tokens/s", "cores": threads,
+                             "sample": f"all {T} tokens, numpy oracle, {threads} threads, median of {reps}"}}
 
 
 def mfma_busy_from_profile() -> dict | None:
@@ -250,6 +272,10 @@ def main(argv=None) -> int:
     M = int(counts.sum())
     hottest = float(counts.max().double() / counts.double().mean())
 
+    # one rank's share of 4-way expert parallelism (its own measurement, run
+    # before the warm-up: the GPU is then already busy when the warm-up starts)
+    c4 = rank_share_detail(dev, args.steps)
+
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -319,11 +345,10 @@ def main(argv=None) -> int:
                      "traffic_source": traffic["source"] if traffic else None,
                      "flops_per_launch": flops_g1, "mean_launch_ms": g1_ms},
         "stages": detail,
-        "c4_rank_share": rank_share_detail(dev, args.steps),
+        "c4_rank_share": c4,
     }
     if not args.no_cpu_baseline:
-        res["cpu_baseline"] = cpu_baseline(layer, min(args.cpu_sample_tokens, T),
-                                           min(args.cpu_single_thread_tokens, T), args.cpu_seconds)
+        res["cpu_baseline"] = cpu_baseline(layer, args.cpu_single_thread_tokens)
     print(json.dumps(res), flush=True)
     return 0
 

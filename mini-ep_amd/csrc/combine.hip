@@ -23,70 +23,36 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kMaxK = 32;
-constexpr int kStage = 1024;   // staged (token, slot) cells per block
 
-template <int DT, bool INDEXED>
-__global__ __launch_bounds__(kThreads) void combine_kernel(const typename Elem<DT>::T* __restrict__ y,
-                                                           const typename Elem<DT>::T* __restrict__ gate,
-                                                           const int32_t* __restrict__ row_of_entry,
-                                                           const uint8_t* __restrict__ valid,
-                                                           int64_t n_tokens, int k, int hidden,
-                                                           typename Elem<DT>::T* __restrict__ out) {
-  typedef typename Elem<DT>::T T;
-  constexpr int EPC = 16 / Elem<DT>::kBytes;
-  const int tpt = hidden / EPC;                         // threads per token
-  const int tokens_per_block = kThreads / tpt;
-  __shared__ float s_gate[kStage];                      // [tokens_per_block * k]
-  __shared__ uint8_t s_here[kStage];
-  __shared__ int32_t s_row[INDEXED ? kStage : 1];       // row of each cell (indexed form)
-  const int tid = threadIdx.x;
-  const int local_tok = tid / tpt;
-  const int c = tid - local_tok * tpt;
-  const int64_t tok0 = static_cast<int64_t>(blockIdx.x) * tokens_per_block;
+// Thread q of the launch owns 16-byte chunk c = q % cpr of token t = q / cpr
+// (cpr = 16-byte chunks per row, any row length that is a multiple of 16 B;
+// n_tokens * cpr < 2^31, checked by the entry point).
+__device__ __forceinline__ bool chunk_of_thread(int64_t n_tokens, int cpr, int64_t& t, int& c) {
+  const uint32_t q = blockIdx.x * static_cast<uint32_t>(kThreads) + threadIdx.x;
+  t = q / static_cast<uint32_t>(cpr);
+  c = static_cast<int>(q - static_cast<uint32_t>(t) * cpr);
+  return t < n_tokens;
+}
 
-  // stage the gates and presence of this block's (token, slot) cells
-  for (int i = tid; i < tokens_per_block * k; i += kThreads) {
-    const int64_t t = tok0 + i / k;
-    bool here = false;
-    float g = 0.0f;
-    if (t < n_tokens && (valid == nullptr || valid[t] != 0) && row_of_entry[t * k + i % k] >= 0) {
-      here = true;
-      g = Elem<DT>::to_f32(gate[t * k + i % k]);
-    }
-    s_gate[i] = g;
-    s_here[i] = here;
-    if constexpr (INDEXED) s_row[i] = here ? row_of_entry[t * k + i % k] : 0;
-  }
-  __syncthreads();
-  const int64_t t = tok0 + local_tok;
-  if (local_tok >= tokens_per_block || t >= n_tokens) return;
-
-  float acc[EPC];
+template <int DT>
+__device__ __forceinline__ void accumulate_cell(float* acc, float g, const u32x4& v) {
+  if constexpr (DT == MEP_DTYPE_BF16) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-  for (int q = 0; q < EPC; ++q) acc[q] = 0.0f;
-  const T* ybase = y + (t * k) * hidden + c * EPC;
-#pragma unroll 8
-  for (int s = 0; s < k; ++s) {
-    if (!s_here[local_tok * k + s]) continue;           // cell computed elsewhere / invalid token
-    const float g = s_gate[local_tok * k + s];
-    const T* ycell;
-    if constexpr (INDEXED) ycell = y + static_cast<int64_t>(s_row[local_tok * k + s]) * hidden + c * EPC;
-    else ycell = ybase + static_cast<int64_t>(s) * hidden;
-    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(ycell));   // read once
-    if constexpr (DT == MEP_DTYPE_BF16) {
-      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        acc[2 * q] += g * bf16_to_f32(static_cast<uint16_t>(w[q] & 0xffffu));
-        acc[2 * q + 1] += g * bf16_to_f32(static_cast<uint16_t>(w[q] >> 16));
-      }
-    } else {
-      acc[0] += g * __uint_as_float(v.x);
-      acc[1] += g * __uint_as_float(v.y);
-      acc[2] += g * __uint_as_float(v.z);
-      acc[3] += g * __uint_as_float(v.w);
+    for (int q = 0; q < 4; ++q) {
+      acc[2 * q] += g * bf16_to_f32(static_cast<uint16_t>(w[q] & 0xffffu));
+      acc[2 * q + 1] += g * bf16_to_f32(static_cast<uint16_t>(w[q] >> 16));
     }
+  } else {
+    acc[0] += g * __uint_as_float(v.x);
+    acc[1] += g * __uint_as_float(v.y);
+    acc[2] += g * __uint_as_float(v.z);
+    acc[3] += g * __uint_as_float(v.w);
   }
+}
+
+template <int DT>
+__device__ __forceinline__ u32x4 pack_row_chunk(const float* acc) {
   u32x4 o;
   if constexpr (DT == MEP_DTYPE_BF16) {
     o.x = pack_bf16x2(acc[0], acc[1]);
@@ -99,7 +65,43 @@ __global__ __launch_bounds__(kThreads) void combine_kernel(const typename Elem<D
     o.z = __float_as_uint(acc[2]);
     o.w = __float_as_uint(acc[3]);
   }
-  *reinterpret_cast<u32x4*>(out + t * hidden + c * EPC) = o;
+  return o;
+}
+
+// Any k: the token's row_of_entry entries and gates are read by each of its
+// threads (the same addresses across the row's threads, served once by the
+// cache); cells are summed in slot order.  INDEXED: cell (t, s) is row
+// row_of_entry[t*k+s] of y (the expert-parallel return path); otherwise it is
+// row t*k+s (the (token, slot) layout GEMM-2 writes).
+template <int DT, bool INDEXED>
+__global__ __launch_bounds__(kThreads) void combine_kernel(const typename Elem<DT>::T* __restrict__ y,
+                                                           const typename Elem<DT>::T* __restrict__ gate,
+                                                           const int32_t* __restrict__ row_of_entry,
+                                                           const uint8_t* __restrict__ valid,
+                                                           int64_t n_tokens, int k, int hidden,
+                                                           typename Elem<DT>::T* __restrict__ out) {
+  typedef typename Elem<DT>::T T;
+  constexpr int EPC = 16 / Elem<DT>::kBytes;
+  int64_t t;
+  int c;
+  if (!chunk_of_thread(n_tokens, hidden / EPC, t, c)) return;
+  const bool tok_ok = valid == nullptr || valid[t] != 0;
+  float acc[EPC];
+#pragma unroll
+  for (int q = 0; q < EPC; ++q) acc[q] = 0.0f;
+  if (tok_ok) {
+#pragma unroll 8
+    for (int s = 0; s < k; ++s) {
+      const int32_t row = row_of_entry[t * k + s];
+      if (row < 0) continue;                            // cell computed elsewhere
+      const float g = Elem<DT>::to_f32(gate[t * k + s]);
+      const int64_t cell = INDEXED ? static_cast<int64_t>(row) : t * k + s;
+      const u32x4 v = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x4*>(y + cell * hidden + c * EPC));   // read once
+      accumulate_cell<DT>(acc, g, v);
+    }
+  }
+  *reinterpret_cast<u32x4*>(out + t * hidden + c * EPC) = pack_row_chunk<DT>(acc);
 }
 
 // k = 8, (token, slot) layout: the 8 cells of a token, its row_of_entry
@@ -117,13 +119,9 @@ __global__ __launch_bounds__(kThreads) void combine8_kernel(const typename Elem<
   typedef typename Elem<DT>::T T;
   constexpr int K = 8;
   constexpr int EPC = 16 / Elem<DT>::kBytes;
-  const int tpt = hidden / EPC;                         // threads per token
-  const int tokens_per_block = kThreads / tpt;
-  const int tid = threadIdx.x;
-  const int local_tok = tid / tpt;
-  const int c = tid - local_tok * tpt;
-  const int64_t t = static_cast<int64_t>(blockIdx.x) * tokens_per_block + local_tok;
-  if (local_tok >= tokens_per_block || t >= n_tokens) return;
+  int64_t t;
+  int c;
+  if (!chunk_of_thread(n_tokens, hidden / EPC, t, c)) return;
   const T* ybase = y + (t * K) * hidden + c * EPC;
   u32x4 v[K];
   // y is read exactly once: non-temporal loads keep these 268 MB (T=16384)
@@ -165,19 +163,7 @@ __global__ __launch_bounds__(kThreads) void combine8_kernel(const typename Elem<
       acc[q] = here ? sum : acc[q];
     }
   }
-  u32x4 o;
-  if constexpr (DT == MEP_DTYPE_BF16) {
-    o.x = pack_bf16x2(acc[0], acc[1]);
-    o.y = pack_bf16x2(acc[2], acc[3]);
-    o.z = pack_bf16x2(acc[4], acc[5]);
-    o.w = pack_bf16x2(acc[6], acc[7]);
-  } else {
-    o.x = __float_as_uint(acc[0]);
-    o.y = __float_as_uint(acc[1]);
-    o.z = __float_as_uint(acc[2]);
-    o.w = __float_as_uint(acc[3]);
-  }
-  *reinterpret_cast<u32x4*>(out + t * hidden + c * EPC) = o;
+  *reinterpret_cast<u32x4*>(out + t * hidden + c * EPC) = pack_row_chunk<DT>(acc);
 }
 
 // out[i, :] = x[perm[i] / top_k, :] (and ids_out[i] = topk_flat[perm[i]]):
@@ -212,17 +198,16 @@ int combine_entry(const char* fn, const void* y, const void* topk_gate, const in
   MEP_REQUIRE(n_tokens >= 0 && top_k >= 1 && top_k <= kMaxK, MEP_ERR_INVALID_ARG,
               "%s: bad n_tokens / top_k %d", fn, top_k);
   const int epc = 16 / dtype_bytes(dtype);
-  MEP_REQUIRE(hidden > 0 && hidden % epc == 0 && hidden / epc <= kThreads &&
-                  kThreads % (hidden / epc) == 0,
-              MEP_ERR_UNSUPPORTED, "%s: hidden %d unsupported for this dtype", fn, hidden);
-  MEP_REQUIRE(kThreads / (hidden / epc) * top_k <= kStage, MEP_ERR_UNSUPPORTED,
-              "%s: hidden %d too small for top_k %d", fn, hidden, top_k);
+  MEP_REQUIRE(hidden > 0 && hidden % epc == 0, MEP_ERR_UNSUPPORTED,
+              "%s: hidden %d is not a multiple of %d for this dtype", fn, hidden, epc);
+  const int64_t cpr = hidden / epc;                    // threads per token row
+  MEP_REQUIRE(n_tokens * cpr < (int64_t(1) << 31), MEP_ERR_UNSUPPORTED,
+              "%s: n_tokens * hidden too large", fn);
   if (n_tokens == 0) return MEP_OK;
   MEP_REQUIRE(y && topk_gate && row_of_entry && out, MEP_ERR_INVALID_ARG, "%s: null pointer", fn);
   MEP_REQUIRE((reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(out)) % 16 == 0,
               MEP_ERR_INVALID_ARG, "%s: y / out must be 16-byte aligned", fn);
-  const int tokens_per_block = kThreads / (hidden / epc);
-  const dim3 grid(static_cast<unsigned>((n_tokens + tokens_per_block - 1) / tokens_per_block));
+  const dim3 grid(static_cast<unsigned>((n_tokens * cpr + kThreads - 1) / kThreads));
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (!INDEXED && top_k == 8) {
     if (dtype == MEP_DTYPE_BF16)

@@ -57,6 +57,8 @@ __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 // ------------------------------------------------------------ host side ----
 void set_error(const char* fmt, ...);
 void clear_error();
+// compute units of the current device (cached per device)
+int device_cu_count();
 
 inline int dtype_bytes(int dtype) {
   return dtype == MEP_DTYPE_F32 ? 4 : (dtype == MEP_DTYPE_BF16 ? 2 : 0);

@@ -75,7 +75,7 @@ struct DispatchParams {
   int seg_block[kMaxSeg + 1];
 };
 
-enum : uint32_t { kFlagRange = 1u, kFlagResident = 2u };
+enum : uint32_t { kFlagRange = 1u, kFlagResident = 2u, kFlagReplicas = 4u };
 
 __device__ __forceinline__ int segment_of_block(const DispatchParams& p, int b) {
   int s = 0;
@@ -92,7 +92,8 @@ __device__ __forceinline__ void block_range(const DispatchParams& p, int b, int 
   if (f1 > p.seg_entry[s + 1]) f1 = p.seg_entry[s + 1];
 }
 
-// Replica count of e clamped to the table width (keeps every table read in bounds).
+// Replica count of e clamped to the table width (keeps every table read in
+// bounds); a count outside [1, rmax] is reported by count_kernel's block 0.
 __device__ __forceinline__ int reps(const DispatchParams& p, int e) {
   const int r = p.n_rep[e];
   return r < 1 ? 1 : (r > p.rmax ? p.rmax : r);
@@ -131,12 +132,19 @@ __global__ __launch_bounds__(kThreads) void count_kernel(DispatchParams p) {
   }
   __syncthreads();
   for (int e = tid; e < p.E; e += kThreads) p.bc[static_cast<int64_t>(b) * p.E + e] = cnt[e];
-  if (tid == 0) p.flags[b] = flag;
+  if (tid == 0 && b != 0) p.flags[b] = flag;
   if (b == 0) {
     if (tid == 0) p.header[0] = static_cast<uint32_t>(p.nbl);
     if (p.has_rep)
       for (int i = tid; i < p.n_seg * p.E; i += kThreads) p.rr_snap[i] = p.rr[i];
+    // every expert needs 1..rmax replicas (ep.py:21: each expert has an owner)
+    for (int e = tid; e < p.E; e += kThreads) {
+      const int r = p.n_rep[e];
+      if (r < 1 || r > p.rmax) atomicOr(&flag, kFlagReplicas);
+    }
   }
+  __syncthreads();
+  if (b == 0 && tid == 0) p.flags[0] = flag;
 }
 
 // One workgroup per expert e: within each source segment, replace the
@@ -415,8 +423,14 @@ extern "C" int mep_dispatch(const int64_t* topk_idx, const uint8_t* valid_mask, 
   MEP_REQUIRE(topk_idx || n_tokens == 0, MEP_ERR_INVALID_ARG, "mep_dispatch: topk_idx is null");
   MEP_REQUIRE(table && n_rep && g2l && offsets && workspace, MEP_ERR_INVALID_ARG,
               "mep_dispatch: null table / n_rep / g2l / offsets / workspace");
-  MEP_REQUIRE((counts && perm && row_of_entry) || n_tokens == 0 || n_local == 0, MEP_ERR_INVALID_ARG,
-              "mep_dispatch: null counts / perm / row_of_entry");
+  // what the kernels write: row_of_entry for every entry, counts for every
+  // local expert, perm for every kept row
+  MEP_REQUIRE(row_of_entry || n_tokens == 0, MEP_ERR_INVALID_ARG,
+              "mep_dispatch: row_of_entry is null (needed whenever n_tokens > 0)");
+  MEP_REQUIRE(counts || n_local == 0, MEP_ERR_INVALID_ARG,
+              "mep_dispatch: counts is null (needed whenever n_local > 0)");
+  MEP_REQUIRE(perm || n_tokens == 0 || n_local == 0, MEP_ERR_INVALID_ARG,
+              "mep_dispatch: perm is null (needed whenever n_tokens > 0 and n_local > 0)");
   MEP_REQUIRE(!has_replicas || rr != nullptr, MEP_ERR_INVALID_ARG,
               "mep_dispatch: rr is required when the layer has replicas");
 
@@ -473,6 +487,8 @@ extern "C" int mep_dispatch_check(const void* workspace, void* stream) {
     MEP_REQUIRE(e == hipSuccess, MEP_ERR_HIP, "mep_dispatch_check: %s", hipGetErrorString(e));
     for (uint32_t j = 0; j < n; ++j) acc |= buf[j];
   }
+  MEP_REQUIRE(!(acc & kFlagReplicas), MEP_ERR_INVALID_ARG,
+              "mep_dispatch: n_rep[e] outside [1, rmax] for some expert (every expert needs an owner)");
   MEP_REQUIRE(!(acc & kFlagRange), MEP_ERR_EXPERT_RANGE,
               "mep_dispatch: expert id outside [0, n_experts) dropped");
   MEP_REQUIRE(!(acc & kFlagResident), MEP_ERR_NOT_RESIDENT,

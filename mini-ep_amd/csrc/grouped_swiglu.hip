@@ -411,13 +411,7 @@ __global__ __launch_bounds__(Cfg::NT) void grouped_gemm_kernel(GemmParams p) {
 
 template <int DT, class Cfg, bool GEMM1>
 hipError_t launch(const GemmParams& p, int64_t max_rows, hipStream_t stream) {
-  static int n_cu = 0;
-  if (n_cu == 0) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n_cu <= 0)
-      n_cu = 256;
-  }
+  const int n_cu = device_cu_count();
   int64_t tiles = ((max_rows + Cfg::BM - 1) / Cfg::BM + p.n_local) * p.n_tiles_n;
   if (tiles == 0) return hipSuccess;
   int64_t grid = tiles < n_cu ? tiles : n_cu;      // one persistent workgroup per CU
@@ -1113,13 +1107,7 @@ __global__ __launch_bounds__(skinny::NT) void moe_gemm_skinny_kernel(GemmParams 
 
 template <bool GEMM1>
 hipError_t launch_bf16(const GemmParams& p, int64_t max_rows, hipStream_t stream) {
-  static int n_cu = 0;
-  if (n_cu == 0) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n_cu <= 0)
-      n_cu = 256;
-  }
+  const int n_cu = device_cu_count();
   if (max_rows <= (GEMM1 ? skinny::kMaxEntries1 : skinny::kMaxEntries2)) {
     // few rows per expert: stream each expert's weights once (same results)
     const int n_cb = GEMM1 ? p.N / 64 : p.N / 128;

@@ -10,7 +10,7 @@ Follows the reference model (miniep/modeling.py):
     router, MoE backend, scaled residual -- :146-197;
   * model: embeddings x ``embedding_multiplier``, final norm, tied LM head
     divided by ``logits_scaling``, optional last-position-only logits -- :218-254;
-  * greedy decoding -- :257-273 (batched here: equal-length prompts decode
+  * greedy decoding -- :249-262 (batched here: equal-length prompts decode
     together, one token per sequence per step).
 Weights use the checkpoint's key names (weights.py:17-26), so a loaded
 checkpoint dict drops in.
@@ -238,27 +238,32 @@ class GraniteMoeModel:
 
 
 def greedy_generate(model: GraniteMoeModel, prompts: torch.Tensor, new_tokens: int,
-                    forced: torch.Tensor | None = None):
+                    forced: torch.Tensor | None = None, return_logits: bool = False):
     """Batched greedy decoding of equal-length prompts (B, T).
 
     Returns (tokens (B, new_tokens), margins (B, new_tokens)): the argmax token
-    of every step and the gap between the best and second-best logit there.
-    With `forced` (B, new_tokens), those tokens are fed back instead of the
-    argmax (teacher forcing), so two models can be compared decision by
-    decision on the same inputs.
+    of every step and the gap between the best and second-best logit there;
+    with ``return_logits`` also the last-position logits of every step
+    (B, new_tokens, V).  With `forced` (B, new_tokens), those tokens are fed
+    back instead of the argmax (teacher forcing), so two models can be
+    compared decision by decision on the same inputs.
     """
     B, T = prompts.shape
     cache = KVCache(model.cfg, B, T + new_tokens, prompts.device)
     logits = model(prompts, cache=cache, logits_at=torch.full((B,), T - 1, device=prompts.device))
-    toks, margins = [], []
+    toks, margins, steps = [], [], []
     for step in range(new_tokens):
-        top2 = logits[:, -1].topk(2, dim=-1)
+        last = logits[:, -1]
+        top2 = last.topk(2, dim=-1)
         toks.append(top2.indices[:, 0])
         margins.append(top2.values[:, 0] - top2.values[:, 1])
+        if return_logits:
+            steps.append(last.clone())
         nxt = toks[-1] if forced is None else forced[:, step]
         if step + 1 < new_tokens:
             logits = model(nxt[:, None], cache=cache)
-    return torch.stack(toks, 1), torch.stack(margins, 1)
+    out = (torch.stack(toks, 1), torch.stack(margins, 1))
+    return out + (torch.stack(steps, 1),) if return_logits else out
 
 
 def build_hip_model(cfg: ModelConfig, weights: dict, check: bool = False) -> GraniteMoeModel:

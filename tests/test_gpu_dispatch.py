@@ -195,3 +195,22 @@ def test_errors_are_reported():
                      seg_tokens=list(range(0, 64, 3)) + [64])
     with pytest.raises(_lib.MepError, match="rr is required"):
         ops.dispatch(_routing(64, 8, E, 6).to(DEV), None, E, table, n_rep, True, None, 0, g2l, E)
+
+
+def test_zero_replica_count_is_reported():
+    """n_rep[e] = 0 (an expert without an owner, which Placement forbids,
+    ep.py:21) is reported by mep_dispatch_check instead of being clamped
+    silently; the launch itself stays in bounds."""
+    banner("dispatch n_rep = 0")
+    E, n, k = 32, 512, 8
+    topk = _routing(n, k, E, 3)
+    table, n_rep, g2l = _world1(E)
+    n_rep[5] = 0
+    with pytest.raises(_lib.MepError, match="n_rep"):
+        ops.dispatch(topk.to(DEV), None, E, table, n_rep, False, None, 0, g2l, E, check=True)
+    n_rep[5] = 2                                          # more replicas than the table has columns
+    with pytest.raises(_lib.MepError, match="n_rep"):
+        ops.dispatch(topk.to(DEV), None, E, table, n_rep, True,
+                     torch.zeros(1, E, dtype=torch.long, device=DEV), 0, g2l, E, check=True)
+    n_rep[5] = 1
+    ops.dispatch(topk.to(DEV), None, E, table, n_rep, False, None, 0, g2l, E, check=True)

@@ -26,6 +26,31 @@ def test_library_exports_every_header_function():
     assert _lib.last_error() == ""
 
 
+def test_dispatch_rejects_missing_outputs_before_launch():
+    """mep_dispatch validates its arguments on the host before anything is
+    enqueued: an output the kernels would write may not be NULL.  (The
+    pointers below are placeholders that are never dereferenced.)"""
+    L = _lib.lib()
+    fake = 4096
+    seg = (ctypes.c_int64 * 2)(0, 64)
+
+    def call(n_tokens, n_local, counts, perm, row):
+        seg[1] = n_tokens
+        return L.mep_dispatch(fake, None, n_tokens, 8, 32, fake, fake, 1, 0, None, seg, 1, 0, fake, n_local,
+                              counts, fake, perm, row, None, None, fake, 1 << 20, None)
+
+    # sender mode (n_local = 0): row_of_entry is still written for every entry
+    assert call(64, 0, None, None, None) == _lib.ERR_INVALID_ARG
+    assert b"row_of_entry" in L.mep_last_error()
+    # no tokens but local experts: counts are still written
+    assert call(0, 4, None, fake, fake) == _lib.ERR_INVALID_ARG
+    assert b"counts" in L.mep_last_error()
+    # tokens and local experts: perm receives the kept rows
+    assert call(64, 4, fake, None, fake) == _lib.ERR_INVALID_ARG
+    assert b"perm" in L.mep_last_error()
+    assert call(64, 4, fake, fake, None) == _lib.ERR_INVALID_ARG
+
+
 def test_workspace_size_queries():
     L = _lib.lib()
     seg = (ctypes.c_int64 * 2)(0, 16384)
@@ -50,6 +75,65 @@ def test_plan_balanced_reproduces_reference_plan(golden_dir):
     # README.md of the reference: 71 replicas in the balanced plan
     assert report["replicas_total"] == 71
     assert all(l["imbalance_after"] <= l["imbalance_before"] for l in report["layers"])
+
+
+def _plan_by_full_resum(counts, world, per, slots_per_rank, target):
+    """A second statement of the planner for the cross-check below: every
+    trial re-sums every rank from scratch, in expert order."""
+    owners = [[e // per] for e in range(len(counts))]
+    slots = [slots_per_rank] * world
+
+    def loads(own):
+        out = [0.0] * world
+        for e, o in enumerate(own):
+            for r in o:
+                out[r] += counts[e] / len(o)
+        return out
+
+    mean = sum(loads(owners)) / world
+    while mean and max(loads(owners)) / mean > target:
+        cur, best = max(loads(owners)), None
+        for e in range(len(counts)):
+            if counts[e] / len(owners[e]) == 0:
+                continue
+            for r in range(world):
+                if r in owners[e] or slots[r] <= 0:
+                    continue
+                trial = [list(o) for o in owners]
+                trial[e] = sorted(trial[e] + [r])
+                m = max(loads(trial))
+                if m < cur and (best is None or m < best[0]):
+                    best = (m, e, r)
+        if best is None:
+            break
+        owners[best[1]] = sorted(owners[best[1]] + [best[2]])
+        slots[best[2]] -= 1
+    return owners
+
+
+@pytest.mark.parametrize("world", [2, 4, 8])
+def test_plan_balanced_matches_full_resummation(world):
+    """The planner re-sums only the ranks a candidate touches; on skewed,
+    tie-heavy random counts its plans equal those of re-summing every rank
+    for every trial."""
+    rng = np.random.default_rng(world)
+    E = 32
+    counts = np.zeros((40, E), dtype=np.int64)
+    for l in range(40):
+        p = np.arange(1, E + 1, dtype=np.float64) ** -rng.uniform(0.3, 1.6)
+        rng.shuffle(p)
+        counts[l] = rng.multinomial(int(rng.integers(50, 5000)), p / p.sum())
+        if l % 5 == 0:
+            counts[l] = (counts[l] // 100) * 100          # many exact ties
+        if l % 7 == 0:
+            counts[l, rng.integers(0, E, 6)] = 0          # idle experts
+    slots, target = (2, 1.05) if world < 8 else (1, 1.02)
+    placement, report = plan_balanced(torch.tensor(counts), world, slots_per_rank=slots,
+                                      target_ratio=target, device="cpu")
+    for l in range(counts.shape[0]):
+        ref = _plan_by_full_resum(counts[l].astype(float).tolist(), world, E // world, slots, target)
+        assert placement.owners[l] == ref, f"layer {l}"
+    assert report["replicas_total"] == sum(len(o) for lay in placement.owners for o in lay) - 40 * E
 
 
 def test_placement_plan_io_and_tables(golden_dir):

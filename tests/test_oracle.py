@@ -13,6 +13,7 @@ import numpy as np
 import pytest
 import torch
 
+from helpers import tie_free
 from oracle import moe_oracle as O
 
 
@@ -294,3 +295,29 @@ def test_mutant_swapped_gate_up_is_caught():
     swapped = np.concatenate([w_in[:, 4:], w_in[:, :4]], axis=1)
     assert not np.allclose(O.experts(x, np.zeros(3, int), swapped, w_out),
                            O.experts(x, np.zeros(3, int), w_in, w_out), rtol=1e-3)
+
+
+def test_torch_cpu_restatement_matches_numpy_oracle():
+    """The PyTorch-CPU restatement that bench.py times as the CPU baseline
+    computes the same layer as the numpy oracle (tie-free routing, masks)."""
+    from oracle import torch_cpu as TC
+    g = torch.Generator().manual_seed(4)
+    n, H, E, I, k = 300, 256, 16, 128, 4
+    x = torch.randn(n, H, generator=g)
+    wr = torch.randn(E, H, generator=g) * 0.05
+    wi = torch.randn(E, 2 * I, H, generator=g) * 0.05
+    wo = torch.randn(E, H, I, generator=g) * 0.05
+    valid = torch.rand(n, generator=g) < 0.8
+    lg = O.router_logits(x.numpy(), wr.numpy())
+    assert tie_free(lg, k)
+    idx, gate = TC.route(x, wr, k)
+    ridx, rgate = O.topk_softmax(lg, k)
+    assert np.array_equal(idx.numpy(), ridx)
+    np.testing.assert_allclose(gate.numpy(), rgate, rtol=1e-5, atol=1e-6)
+    out = TC.moe_local(x, idx, gate, wi, wo, valid).numpy()
+    ref = O.moe_layer_local(x.numpy(), ridx, rgate, wi.numpy(), wo.numpy(), valid.numpy())
+    assert np.abs(out - ref).max() <= 1e-5 * np.abs(ref).max()
+    assert (out[~valid.numpy()] == 0).all()
+    # a planted mistake (gate and up halves swapped) is caught by the same check
+    bad = TC.moe_local(x, idx, gate, torch.cat([wi[:, I:], wi[:, :I]], 1), wo, valid).numpy()
+    assert np.abs(bad - ref).max() > 1e-2 * np.abs(ref).max()
