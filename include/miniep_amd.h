@@ -128,8 +128,38 @@ int mep_dispatch(const int64_t* topk_idx, const uint8_t* valid_mask, int64_t n_t
                  void* workspace, size_t workspace_bytes, void* stream);
 
 /* Synchronises `stream` and returns MEP_ERR_EXPERT_RANGE / MEP_ERR_NOT_RESIDENT
- * if the last mep_dispatch on `workspace` dropped entries, else MEP_OK. */
+ * if the last mep_dispatch on `workspace` dropped entries, MEP_ERR_INVALID_ARG
+ * if some n_rep[e] lay outside [1, rmax] (the kernels then clamp it), else
+ * MEP_OK. */
 int mep_dispatch_check(const void* workspace, void* stream);
+
+/* Status bits of mep_dispatch_noalloc (and of the conditions mep_dispatch_check reports). */
+#define MEP_DISPATCH_STATUS_RANGE 1u          /* an expert id outside [0, n_experts) was dropped      */
+#define MEP_DISPATCH_STATUS_NOT_RESIDENT 2u   /* an entry for a non-resident expert was dropped      */
+#define MEP_DISPATCH_STATUS_REPLICAS 4u       /* some n_rep[e] lies outside [1, rmax]                 */
+
+/* mep_dispatch without a workspace argument: it allocates nothing and takes
+ * no workspace.  No counterpart in the reference; it is for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving loops
+ * or harnesses that forbid hipMalloc).  Same arguments, kernels and results
+ * as mep_dispatch; the workspace is a static device array of this library,
+ * 2 MiB per GPU, held until the process ends, and its address is looked up
+ * once per device on the first call there.  Calls whose workspace would
+ * exceed 2 MiB (mep_dispatch_workspace_size) return MEP_ERR_UNSUPPORTED: e.g.
+ * up to 2^21 entries (N*k) with 32 experts.  All calls on one GPU share that
+ * array, so calls that overlap on one GPU (different streams) race: serialise
+ * them.  `status` (device uint32, may be NULL) receives the OR of the
+ * MEP_DISPATCH_STATUS_* conditions of this call, written by the kernels
+ * (mep_dispatch_check is not available for this form). */
+int mep_dispatch_noalloc(const int64_t* topk_idx, const uint8_t* valid_mask, int64_t n_tokens,
+                         int32_t top_k, int32_t n_experts,
+                         const int32_t* table, const int32_t* n_rep, int32_t rmax,
+                         int32_t has_replicas, int64_t* rr,
+                         const int64_t* seg_tokens /* host */, int32_t n_segments,
+                         int32_t my_rank, const int32_t* g2l, int32_t n_local,
+                         int32_t* counts, int32_t* offsets, int32_t* perm,
+                         int32_t* row_of_entry, int32_t* dest, int64_t* route_counts,
+                         uint32_t* status, void* stream);
 
 /* ------------------------------------------------------------------------
  * Grouped SwiGLU experts over the dispatched rows (run_experts,

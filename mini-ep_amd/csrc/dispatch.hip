@@ -34,6 +34,8 @@
 //                   counts, offsets, route_counts and the updated rr.
 #include "common.h"
 
+#include <atomic>
+
 namespace mep {
 namespace {
 
@@ -63,6 +65,7 @@ struct DispatchParams {
   int32_t* row_of_entry;
   int32_t* dest;
   int64_t* route_counts;
+  uint32_t* status;     // optional device word: OR of the flags of this call
   // workspace
   uint32_t* header;     // [0] = number of launched blocks
   uint32_t* flags;      // [2 * nbl]: count-kernel flags, scatter-kernel flags
@@ -134,7 +137,10 @@ __global__ __launch_bounds__(kThreads) void count_kernel(DispatchParams p) {
   for (int e = tid; e < p.E; e += kThreads) p.bc[static_cast<int64_t>(b) * p.E + e] = cnt[e];
   if (tid == 0 && b != 0) p.flags[b] = flag;
   if (b == 0) {
-    if (tid == 0) p.header[0] = static_cast<uint32_t>(p.nbl);
+    if (tid == 0) {
+      p.header[0] = static_cast<uint32_t>(p.nbl);
+      if (p.status != nullptr) *p.status = 0u;      // the scatter kernel ORs into it
+    }
     if (p.has_rep)
       for (int i = tid; i < p.n_seg * p.E; i += kThreads) p.rr_snap[i] = p.rr[i];
     // every expert needs 1..rmax replicas (ep.py:21: each expert has an owner)
@@ -349,7 +355,13 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(DispatchParams p) {
     p.row_of_entry[f] = row;
   }
   __syncthreads();
-  if (tid == 0) p.flags[p.nbl + b] = flag;
+  if (tid == 0) {
+    p.flags[p.nbl + b] = flag;
+    if (p.status != nullptr) {
+      const uint32_t f = flag | p.flags[b];         // this block's count and scatter flags
+      if (f != 0u) atomicOr(p.status, f);
+    }
+  }
 }
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
@@ -395,57 +407,103 @@ extern "C" size_t mep_dispatch_workspace_size(int64_t n_tokens, int32_t top_k, i
   return ws_layout(nb > 0 ? nb : 1, n_segments, n_experts).total;
 }
 
-extern "C" int mep_dispatch(const int64_t* topk_idx, const uint8_t* valid_mask, int64_t n_tokens,
-                            int32_t top_k, int32_t n_experts, const int32_t* table,
-                            const int32_t* n_rep, int32_t rmax, int32_t has_replicas, int64_t* rr,
-                            const int64_t* seg_tokens, int32_t n_segments, int32_t my_rank,
-                            const int32_t* g2l, int32_t n_local, int32_t* counts, int32_t* offsets,
-                            int32_t* perm, int32_t* row_of_entry, int32_t* dest,
-                            int64_t* route_counts, void* workspace, size_t workspace_bytes,
-                            void* stream) {
+namespace mep {
+
+// Static scratch of mep_dispatch_noalloc: the workspace of mep_dispatch
+// (header, flags, counter snapshot, per-block histograms, segment totals) in
+// a file-scope device array, one copy per GPU, held until the process ends.
+// Every call on a GPU reuses that GPU's copy; the kernels write every word
+// they later read, so nothing needs clearing between calls.
+constexpr size_t kScratchBytes = size_t(2) << 20;
+__device__ __attribute__((aligned(256))) unsigned char dispatch_scratch[kScratchBytes];
+
+namespace {
+
+// Device address of `dispatch_scratch` on the current device, looked up on the first
+// call on each device (hipGetSymbolAddress with that device current) and kept
+// per device.  The array's name is only a host-side handle; kernels receive
+// this address.
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch[kMaxDevices];
+
+int scratch_address(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  MEP_REQUIRE(e == hipSuccess, MEP_ERR_HIP, "mep_dispatch_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+  MEP_REQUIRE(dev >= 0 && dev < kMaxDevices, MEP_ERR_UNSUPPORTED,
+              "mep_dispatch_noalloc: device %d beyond the %d supported", dev, kMaxDevices);
+  void* ptr = g_scratch[dev].load(std::memory_order_acquire);
+  if (ptr == nullptr) {
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(dispatch_scratch));
+    MEP_REQUIRE(e == hipSuccess && ptr != nullptr, MEP_ERR_HIP,
+                "mep_dispatch_noalloc: hipGetSymbolAddress(dispatch_scratch): %s", hipGetErrorString(e));
+    g_scratch[dev].store(ptr, std::memory_order_release);
+  }
+  *out = ptr;
+  return MEP_OK;
+}
+
+// Shared body of mep_dispatch and mep_dispatch_noalloc.  workspace == NULL
+// selects the static scratch (whose size bounds the call).
+int dispatch_impl(const char* fn, const int64_t* topk_idx, const uint8_t* valid_mask, int64_t n_tokens,
+                  int32_t top_k, int32_t n_experts, const int32_t* table, const int32_t* n_rep, int32_t rmax,
+                  int32_t has_replicas, int64_t* rr, const int64_t* seg_tokens, int32_t n_segments,
+                  int32_t my_rank, const int32_t* g2l, int32_t n_local, int32_t* counts, int32_t* offsets,
+                  int32_t* perm, int32_t* row_of_entry, int32_t* dest, int64_t* route_counts,
+                  uint32_t* status, void* workspace, size_t workspace_bytes, void* stream) {
   clear_error();
+  const bool use_scratch = workspace == nullptr;
   MEP_REQUIRE(n_tokens >= 0 && top_k >= 1 && top_k <= 32, MEP_ERR_INVALID_ARG,
-              "mep_dispatch: bad n_tokens %lld / top_k %d", (long long)n_tokens, top_k);
+              "%s: bad n_tokens %lld / top_k %d", fn, (long long)n_tokens, top_k);
   MEP_REQUIRE(n_experts >= 1 && n_experts <= kMaxExperts, MEP_ERR_UNSUPPORTED,
-              "mep_dispatch: n_experts %d outside [1, %d]", n_experts, kMaxExperts);
+              "%s: n_experts %d outside [1, %d]", fn, n_experts, kMaxExperts);
   MEP_REQUIRE(n_tokens * top_k < (int64_t(1) << 31), MEP_ERR_UNSUPPORTED,
-              "mep_dispatch: n_tokens * top_k must be < 2^31");
-  MEP_REQUIRE(rmax >= 1, MEP_ERR_INVALID_ARG, "mep_dispatch: rmax %d < 1", rmax);
+              "%s: n_tokens * top_k must be < 2^31", fn);
+  MEP_REQUIRE(rmax >= 1, MEP_ERR_INVALID_ARG, "%s: rmax %d < 1", fn, rmax);
   MEP_REQUIRE(n_local >= 0 && n_local <= n_experts, MEP_ERR_INVALID_ARG,
-              "mep_dispatch: n_local %d outside [0, %d]", n_local, n_experts);
+              "%s: n_local %d outside [0, %d]", fn, n_local, n_experts);
   MEP_REQUIRE(n_segments >= 1 && n_segments <= kMaxSeg && seg_tokens != nullptr,
-              MEP_ERR_INVALID_ARG, "mep_dispatch: need 1..%d segments (got %d)", kMaxSeg, n_segments);
+              MEP_ERR_INVALID_ARG, "%s: need 1..%d segments (got %d)", fn, kMaxSeg, n_segments);
   MEP_REQUIRE(seg_tokens[0] == 0 && seg_tokens[n_segments] == n_tokens, MEP_ERR_INVALID_ARG,
-              "mep_dispatch: seg_tokens must run from 0 to n_tokens");
+              "%s: seg_tokens must run from 0 to n_tokens", fn);
   for (int s = 0; s < n_segments; ++s)
     MEP_REQUIRE(seg_tokens[s + 1] >= seg_tokens[s], MEP_ERR_INVALID_ARG,
-                "mep_dispatch: seg_tokens must be non-decreasing");
-  MEP_REQUIRE(topk_idx || n_tokens == 0, MEP_ERR_INVALID_ARG, "mep_dispatch: topk_idx is null");
-  MEP_REQUIRE(table && n_rep && g2l && offsets && workspace, MEP_ERR_INVALID_ARG,
-              "mep_dispatch: null table / n_rep / g2l / offsets / workspace");
+                "%s: seg_tokens must be non-decreasing", fn);
+  MEP_REQUIRE(topk_idx || n_tokens == 0, MEP_ERR_INVALID_ARG, "%s: topk_idx is null", fn);
+  MEP_REQUIRE(table && n_rep && g2l && offsets, MEP_ERR_INVALID_ARG,
+              "%s: null table / n_rep / g2l / offsets", fn);
   // what the kernels write: row_of_entry for every entry, counts for every
   // local expert, perm for every kept row
   MEP_REQUIRE(row_of_entry || n_tokens == 0, MEP_ERR_INVALID_ARG,
-              "mep_dispatch: row_of_entry is null (needed whenever n_tokens > 0)");
+              "%s: row_of_entry is null (needed whenever n_tokens > 0)", fn);
   MEP_REQUIRE(counts || n_local == 0, MEP_ERR_INVALID_ARG,
-              "mep_dispatch: counts is null (needed whenever n_local > 0)");
+              "%s: counts is null (needed whenever n_local > 0)", fn);
   MEP_REQUIRE(perm || n_tokens == 0 || n_local == 0, MEP_ERR_INVALID_ARG,
-              "mep_dispatch: perm is null (needed whenever n_tokens > 0 and n_local > 0)");
+              "%s: perm is null (needed whenever n_tokens > 0 and n_local > 0)", fn);
   MEP_REQUIRE(!has_replicas || rr != nullptr, MEP_ERR_INVALID_ARG,
-              "mep_dispatch: rr is required when the layer has replicas");
+              "%s: rr is required when the layer has replicas", fn);
 
   DispatchParams p;
   p.nb = count_blocks(seg_tokens, n_segments, top_k, p.seg_block);
   p.nbl = p.nb > 0 ? p.nb : 1;
   const WsLayout l = ws_layout(p.nbl, n_segments, n_experts);
-  MEP_REQUIRE(workspace_bytes >= l.total, MEP_ERR_WORKSPACE,
-              "mep_dispatch: workspace %zu B < required %zu B", workspace_bytes, l.total);
+  if (use_scratch) {
+    MEP_REQUIRE(l.total <= kScratchBytes, MEP_ERR_UNSUPPORTED,
+                "%s: needs %zu B of scratch, more than the %zu B static scratch (fewer tokens or experts per call)",
+                fn, l.total, kScratchBytes);
+    const int rc = scratch_address(&workspace);
+    if (rc != MEP_OK) return rc;
+  } else {
+    MEP_REQUIRE(workspace_bytes >= l.total, MEP_ERR_WORKSPACE,
+                "%s: workspace %zu B < required %zu B", fn, workspace_bytes, l.total);
+  }
   char* ws = static_cast<char*>(workspace);
   p.topk_idx = topk_idx; p.valid = valid_mask; p.n_tokens = n_tokens;
   p.k = top_k; p.E = n_experts; p.table = table; p.n_rep = n_rep; p.rmax = rmax;
   p.has_rep = has_replicas ? 1 : 0; p.rr = rr; p.my_rank = my_rank; p.g2l = g2l;
   p.n_local = n_local; p.counts = counts; p.offsets = offsets; p.perm = perm;
   p.row_of_entry = row_of_entry; p.dest = dest; p.route_counts = route_counts;
+  p.status = status;
   p.header = reinterpret_cast<uint32_t*>(ws + l.header);
   p.flags = reinterpret_cast<uint32_t*>(ws + l.flags);
   p.rr_snap = reinterpret_cast<int64_t*>(ws + l.rr_snap);
@@ -468,6 +526,39 @@ extern "C" int mep_dispatch(const int64_t* topk_idx, const uint8_t* valid_mask, 
   return MEP_OK;
 }
 
+}  // namespace
+}  // namespace mep
+
+extern "C" int mep_dispatch(const int64_t* topk_idx, const uint8_t* valid_mask, int64_t n_tokens,
+                            int32_t top_k, int32_t n_experts, const int32_t* table,
+                            const int32_t* n_rep, int32_t rmax, int32_t has_replicas, int64_t* rr,
+                            const int64_t* seg_tokens, int32_t n_segments, int32_t my_rank,
+                            const int32_t* g2l, int32_t n_local, int32_t* counts, int32_t* offsets,
+                            int32_t* perm, int32_t* row_of_entry, int32_t* dest,
+                            int64_t* route_counts, void* workspace, size_t workspace_bytes,
+                            void* stream) {
+  if (workspace == nullptr) {
+    clear_error();
+    set_error("mep_dispatch: null workspace");
+    return MEP_ERR_INVALID_ARG;
+  }
+  return dispatch_impl("mep_dispatch", topk_idx, valid_mask, n_tokens, top_k, n_experts, table, n_rep, rmax,
+                       has_replicas, rr, seg_tokens, n_segments, my_rank, g2l, n_local, counts, offsets, perm,
+                       row_of_entry, dest, route_counts, nullptr, workspace, workspace_bytes, stream);
+}
+
+extern "C" int mep_dispatch_noalloc(const int64_t* topk_idx, const uint8_t* valid_mask, int64_t n_tokens,
+                                    int32_t top_k, int32_t n_experts, const int32_t* table,
+                                    const int32_t* n_rep, int32_t rmax, int32_t has_replicas, int64_t* rr,
+                                    const int64_t* seg_tokens, int32_t n_segments, int32_t my_rank,
+                                    const int32_t* g2l, int32_t n_local, int32_t* counts, int32_t* offsets,
+                                    int32_t* perm, int32_t* row_of_entry, int32_t* dest,
+                                    int64_t* route_counts, uint32_t* status, void* stream) {
+  return dispatch_impl("mep_dispatch_noalloc", topk_idx, valid_mask, n_tokens, top_k, n_experts, table, n_rep,
+                       rmax, has_replicas, rr, seg_tokens, n_segments, my_rank, g2l, n_local, counts, offsets,
+                       perm, row_of_entry, dest, route_counts, status, nullptr, 0, stream);
+}
+
 extern "C" int mep_dispatch_check(const void* workspace, void* stream) {
   clear_error();
   MEP_REQUIRE(workspace != nullptr, MEP_ERR_INVALID_ARG, "mep_dispatch_check: null workspace");
@@ -487,6 +578,9 @@ extern "C" int mep_dispatch_check(const void* workspace, void* stream) {
     MEP_REQUIRE(e == hipSuccess, MEP_ERR_HIP, "mep_dispatch_check: %s", hipGetErrorString(e));
     for (uint32_t j = 0; j < n; ++j) acc |= buf[j];
   }
+  static_assert(kFlagRange == MEP_DISPATCH_STATUS_RANGE && kFlagResident == MEP_DISPATCH_STATUS_NOT_RESIDENT &&
+                    kFlagReplicas == MEP_DISPATCH_STATUS_REPLICAS,
+                "status bits of the header");
   MEP_REQUIRE(!(acc & kFlagReplicas), MEP_ERR_INVALID_ARG,
               "mep_dispatch: n_rep[e] outside [1, rmax] for some expert (every expert needs an owner)");
   MEP_REQUIRE(!(acc & kFlagRange), MEP_ERR_EXPERT_RANGE,

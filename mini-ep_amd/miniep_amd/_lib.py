@@ -23,6 +23,10 @@ ERR_EXPERT_RANGE = -4
 ERR_NOT_RESIDENT = -5
 ERR_HIP = -6
 
+DISPATCH_STATUS_RANGE = 1
+DISPATCH_STATUS_NOT_RESIDENT = 2
+DISPATCH_STATUS_REPLICAS = 4
+
 
 class MepError(RuntimeError):
     """A C-ABI call returned a nonzero status."""
@@ -60,6 +64,11 @@ _SIGNATURES = {
                                     _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                     _c_void_p, _c_void_p, _size, _c_void_p]),
     "mep_dispatch_check": (ctypes.c_int, [_c_void_p, _c_void_p]),
+    "mep_dispatch_noalloc": (ctypes.c_int, [_c_void_p, _c_void_p, _i64, _i32, _i32,
+                                            _c_void_p, _c_void_p, _i32, _i32, _c_void_p,
+                                            ctypes.POINTER(_i64), _i32, _i32, _c_void_p, _i32,
+                                            _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                            _c_void_p, _c_void_p, _c_void_p]),
     "mep_experts_workspace_size": (_size, [_i64, _i32, _i32]),
     "mep_grouped_swiglu": (ctypes.c_int, [_c_void_p, _i64, _i32, _c_void_p, _c_void_p, _i32,
                                           _i64, _c_void_p, _c_void_p, _i32, _i32, _i32,

@@ -19,7 +19,7 @@ from oracle import moe_oracle as O
 def test_library_exports_every_header_function():
     L = _lib.lib()
     names = _lib.header_functions()
-    assert len(names) == 14
+    assert len(names) == 15
     for n in names:
         assert hasattr(L, n), n
     assert L.mep_abi_version() == 2
@@ -162,3 +162,17 @@ def test_ops_reject_cpu_tensors():
     from miniep_amd import ops
     with pytest.raises(RuntimeError, match="GPU only"):
         ops.router_topk(torch.zeros(4, 256), torch.zeros(32, 256), 8)
+
+
+def test_dispatch_noalloc_rejects_calls_beyond_its_scratch():
+    """The allocation-free dispatch checks its size limit on the host, before
+    it touches the device: 2^22 entries with 256 experts need more than the
+    2 MiB static scratch."""
+    L = _lib.lib()
+    fake = 4096
+    n = 1 << 19
+    seg = (ctypes.c_int64 * 2)(0, n)
+    assert L.mep_dispatch_workspace_size(n, 8, 256, 1, seg) > (2 << 20)
+    rc = L.mep_dispatch_noalloc(fake, None, n, 8, 256, fake, fake, 1, 0, None, seg, 1, 0, fake, 256,
+                                fake, fake, fake, fake, None, None, None, None)
+    assert rc == _lib.ERR_UNSUPPORTED and b"static scratch" in L.mep_last_error()
