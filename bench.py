@@ -33,9 +33,12 @@ hardware's own view from the committed counter summary
 (``profiles/*mfma_busy*.md``: MFMA busy cycles over active cycles).
 ``c4_rank_share`` (measured before the warm-up, outside the timed region):
 one rank's share of 4-way expert parallelism under the reference's balanced
-plan at T=8192, per rank.  Order of the run: calibration copy, one routing
-pass, c4_rank_share, `warmup` steps, the `steps` timed steps, the per-stage
-pass, cpu_baseline.
+plan at T=8192, per rank.  ``rebalance`` (also before the warm-up): the live
+swap of 24 layers' expert weights from the naive placement to the
+reference's balanced plan, 4 ranks' expert stores, copied experts and time.
+Order of the run: calibration copy, one routing pass, c4_rank_share,
+rebalance, `warmup` steps, the `steps` timed steps, the per-stage pass,
+cpu_baseline.
 ``cpu_baseline`` times the reference's algorithm restated in PyTorch-CPU
 (fp32) on the same workload on the host's CPU share (and on one core), with
 the numpy oracle's figure beside it.
@@ -191,6 +194,37 @@ def rank_share_detail(dev, steps: int) -> dict:
             "measures": "dispatch (share mode) + GEMM-1 + GEMM-2 per call, back to back", "ranks": ranks}
 
 
+def rebalance_detail(dev) -> dict:
+    """Live re-placement timed (server.py:51-62 / :166-183 apply_seconds):
+    4 ranks' ExpertStores (10 slots per layer: 8 owned + 2 replica slots)
+    hold the naive placement of 24 GraniteMoE layers; swapping in the
+    reference's balanced plan copies only the arriving experts (its 71
+    replicas) from a device-resident bf16 checkpoint of all experts, one
+    mep_copy_experts launch per layer and rank; timed with the device work."""
+    import torch
+
+    from miniep_amd import ExpertStore, Placement, apply_placement, workloads
+
+    H, I, E, NL = workloads.HIDDEN, workloads.INTER, workloads.EXPERTS, 24
+    g = torch.Generator(device=dev).manual_seed(13)
+    ck_in = [torch.randn(E, 2 * I, H, generator=g, device=dev).mul_(0.02).to(torch.bfloat16) for _ in range(NL)]
+    ck_out = [torch.randn(E, H, I, generator=g, device=dev).mul_(0.02).to(torch.bfloat16) for _ in range(NL)]
+    naive = Placement.naive(NL, E, 4, device=dev)
+    balanced = Placement.from_plan(json.loads((ROOT / "tests/golden/plan_balanced.json").read_text()), device=dev)
+    stores = [ExpertStore(NL, 10, H, I, torch.bfloat16, dev) for _ in range(4)]
+    for r, st in enumerate(stores):
+        apply_placement([], st, naive, r, lambda l: (ck_in[l], ck_out[l]))
+    res = [apply_placement([], st, balanced, r, lambda l: (ck_in[l], ck_out[l])) for r, st in enumerate(stores)]
+    copied = sum(x["copied"] for x in res)
+    ms = 1e3 * sum(x["seconds"] for x in res)
+    return {"what": "naive -> reference balanced plan, 4 ranks x 24 layers, bf16 experts from a device-resident "
+                    "checkpoint (ExpertStore.assign: mep_copy_experts of the arriving experts only)",
+            "experts_copied": copied, "bytes_copied": copied * 3 * H * I * 2, "ms": ms,
+            "per_rank_ms": [1e3 * x["seconds"] for x in res],
+            "reference_context": "reference /rebalance apply_seconds ~1 s for 66 replicas on its 4-rank CPU "
+                                 "cluster, re-reading safetensors (README.md:42-43)"}
+
+
 def traffic_from_profile() -> dict | None:
     """GEMM-1 HBM bytes per launch from the committed counter summary, if any."""
     for f in sorted((ROOT / "profiles").glob("*hbm_traffic.md")):
@@ -275,6 +309,8 @@ def main(argv=None) -> int:
     # one rank's share of 4-way expert parallelism (its own measurement, run
     # before the warm-up: the GPU is then already busy when the warm-up starts)
     c4 = rank_share_detail(dev, args.steps)
+    rebalance = rebalance_detail(dev)
+    torch.cuda.empty_cache()
 
     for _ in range(args.warmup):
         step()
@@ -346,6 +382,7 @@ def main(argv=None) -> int:
                      "flops_per_launch": flops_g1, "mean_launch_ms": g1_ms},
         "stages": detail,
         "c4_rank_share": c4,
+        "rebalance": rebalance,
     }
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(layer, args.cpu_single_thread_tokens)

@@ -204,6 +204,32 @@ int mep_swiglu_down(const void* act, int64_t n_tokens, int32_t top_k, const int3
                     const void* w_out, int32_t hidden, int32_t inter, int32_t dtype,
                     void* y_entries, int32_t* tile_queue, void* stream);
 
+/* Expert weight slots (the live re-slice of server.py:51-62 / weights.py:37-61
+ * without re-reading a checkpoint for experts that stay):
+ *   mep_grouped_swiglu_slots  mep_grouped_swiglu with local expert j's weights
+ *                             in slot w_slot[j] of w_in (n_slots, 2I, H) /
+ *                             w_out (n_slots, H, I); w_slot (n_local,) int32
+ *                             device.  Same kernels and results.
+ *   mep_copy_experts          for i < n: slot dst_slot[i] of (dst_in, dst_out)
+ *                             = expert src_index[i] of (src_in, src_out), both
+ *                             in the layouts above (src: n_src experts in
+ *                             device memory, e.g. this layer's checkpoint
+ *                             tensors kept in HBM).  src_index / dst_slot
+ *                             are host arrays, checked
+ *                             before anything is enqueued; a slot may be named
+ *                             once per call. */
+int mep_grouped_swiglu_slots(const void* x, int64_t n_tokens, int32_t top_k,
+                             const int32_t* perm, const int32_t* offsets, int32_t n_local,
+                             int64_t max_rows, const void* w_in, const void* w_out,
+                             const int32_t* w_slot, int32_t hidden, int32_t inter, int32_t dtype,
+                             void* y_entries, void* workspace, size_t workspace_bytes,
+                             int32_t* tile_queue, void* stream);
+
+int mep_copy_experts(const void* src_in, const void* src_out, int32_t n_src,
+                     void* dst_in, void* dst_out, int32_t n_slots,
+                     const int32_t* src_index /* host */, const int32_t* dst_slot /* host */,
+                     int32_t n, int32_t hidden, int32_t inter, int32_t dtype, void* stream);
+
 /* ------------------------------------------------------------------------
  * Combine: out[t] = sum_{s=0..k-1, row_of_entry[t*k+s] >= 0} gate[t,s] * y_entries[t*k+s]
  * summed in slot order in fp32, stored in `dtype`; invalid tokens give 0.

@@ -70,6 +70,7 @@ struct GemmParams {
   const void* W;             // GEMM-1: w_in (n_local, 2N, K); GEMM-2: w_out (n_local, N, K)
   void* C;                   // GEMM-1: act (max_rows, N); GEMM-2: y_entries (N*k, N)
   int64_t w_expert_stride;   // elements per expert in W
+  const int32_t* w_slot;     // (n_local,) slot of local expert j in W, or NULL: slot j
   int n_local, top_k;
   int K;                     // reduction length
   int N;                     // output columns (GEMM-1: I; GEMM-2: H)
@@ -236,7 +237,8 @@ __global__ __launch_bounds__(Cfg::NT) void grouped_gemm_kernel(GemmParams p) {
         src_off[i] = static_cast<uint32_t>((src_row * K + lchunk_v * EPC) * EB);
       }
     } else {
-      g_base = static_cast<const unsigned char*>(p.W) + static_cast<int64_t>(t.e) * p.w_expert_stride * EB;
+      const int slot = p.w_slot != nullptr ? p.w_slot[t.e] : t.e;
+      g_base = static_cast<const unsigned char*>(p.W) + static_cast<int64_t>(slot) * p.w_expert_stride * EB;
 #pragma unroll
       for (int i = 0; i < BPW; ++i) {
         const int rb = (wave * BPW + i) * 8 + lrow_v - BM;
@@ -471,7 +473,7 @@ constexpr int NLMAX = 256;
 // after the stage buffers; the tables follow it
 constexpr int STG_ROWS = 8, STG_WAVE = STG_ROWS * 256, STG = 4 * HALF;
 constexpr int TABLES = STG + NW * STG_WAVE;
-constexpr int LDS_BYTES = TABLES + (2 * (NLMAX + 1) + 2 * BM + 2) * 4;
+constexpr int LDS_BYTES = TABLES + (2 * (NLMAX + 1) + 2 * BM + 2 + NLMAX) * 4;
 static_assert(LDS_BYTES <= 160 * 1024, "LDS budget of one workgroup");
 // buffer resource word 3 for raw 32-bit buffer access on gfx9-family parts
 constexpr int kBufWord3 = 0x00020000;
@@ -522,6 +524,7 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
   int* const s_off = s_prefix + NLMAX + 1;                             // [NLMAX + 1] row offsets
   int* const s_rows = s_off + NLMAX + 1;                               // [2][BM] row maps
   int* const s_pool = s_rows + 2 * BM;                                 // [2] pool items taken
+  int* const s_slot = s_pool + 2;                                      // [NLMAX] weight slot of expert j
 
   const int tid = threadIdx.x;
   // wave index as a scalar: keeps per-wave choices (A or weight rows, buffer
@@ -535,6 +538,7 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
 
   // ---- tile table ---------------------------------------------------------------
   for (int j = tid; j <= nl; j += NT) s_off[j] = p.offsets[j];
+  for (int j = tid; j < nl; j += NT) s_slot[j] = p.w_slot != nullptr ? p.w_slot[j] : j;
   __syncthreads();
   if (tid < 64) scan_units<BM>(s_off, s_prefix, nl, p.n_tiles_n);
   __syncthreads();
@@ -581,7 +585,7 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
   // nothing.  A tile with at most 128 rows (an expert's last, partial one) is
   // a row half: the 4 waves of rows 0..127, one per SIMD, compute it, and a
   // row half sums every output element in the same order as a whole tile.
-  struct Tile { int e, row0, row_end, valid_end, nt, act_wm; };
+  struct Tile { int e, slot, row0, row_end, valid_end, nt, act_wm; };
   auto decode_tile = [&](int lt) {
     int lo = 0, hi = nl - 1;                       // largest j with s_prefix[j] <= lt
     while (lo < hi) {
@@ -591,6 +595,7 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
     const int u = lt - s_prefix[lo];
     Tile t;                                        // uniform: keep it in SGPRs
     t.e = __builtin_amdgcn_readfirstlane(lo);
+    t.slot = __builtin_amdgcn_readfirstlane(s_slot[lo]);
     t.row0 = __builtin_amdgcn_readfirstlane(s_off[lo] + (u / p.n_tiles_n) * BM);
     t.row_end = __builtin_amdgcn_readfirstlane(s_off[lo + 1]);
     t.nt = __builtin_amdgcn_readfirstlane(u % p.n_tiles_n);
@@ -659,7 +664,7 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
       // loads read past a zero-sized buffer, i.e. zeros, without memory traffic
       if (t.act_wm < 4 && wv * BPW * 8 >= t.act_wm * 64) s.bytes = 0;
     } else {
-      s.base = static_cast<const unsigned char*>(p.W) + static_cast<int64_t>(t.e) * p.w_expert_stride * 2;
+      s.base = static_cast<const unsigned char*>(p.W) + static_cast<int64_t>(t.slot) * p.w_expert_stride * 2;
       s.bytes = static_cast<int>(p.w_expert_stride * 2);
       // weight row of stage row rb0 + lrow (rb0 = the block's first row, a
       // multiple of 8): pair_cols(rb0) + lane part, so the row split into a
@@ -1016,7 +1021,8 @@ __global__ __launch_bounds__(skinny::NT) void moe_gemm_skinny_kernel(GemmParams 
   const int nt = cb / 2;
   const int rot = (!GEMM1 && KD % 4 == 0) ? 2 * (nt & 3) * (KD / 4) : 0;
   // weight rows of this wave's two fragments
-  const T* W = static_cast<const T*>(p.W) + static_cast<int64_t>(e) * p.w_expert_stride;
+  const int slot = p.w_slot != nullptr ? p.w_slot[e] : e;
+  const T* W = static_cast<const T*>(p.W) + static_cast<int64_t>(slot) * p.w_expert_stride;
   int wrow[2];
   if constexpr (GEMM1) {
     const int g0 = cb * 64 + wave * 16;
@@ -1133,10 +1139,11 @@ typedef TileCfg<128, 128, 2, 2> CfgF32;
 
 template <int DT, class Cfg>
 int run_gate_up(const void* x, int64_t n_tokens, int top_k, const int32_t* perm, const int32_t* offsets,
-                int n_local, int64_t max_rows, const void* w_in, int hidden, int inter, void* act,
-                int32_t* tile_queue, hipStream_t stream) {
+                int n_local, int64_t max_rows, const void* w_in, const int32_t* w_slot, int hidden, int inter,
+                void* act, int32_t* tile_queue, hipStream_t stream) {
   GemmParams g1;
   g1.A = x; g1.perm = perm; g1.offsets = offsets; g1.W = w_in; g1.C = act; g1.tile_queue = tile_queue;
+  g1.w_slot = w_slot;
   g1.w_expert_stride = static_cast<int64_t>(2) * inter * hidden;
   g1.n_local = n_local; g1.top_k = top_k; g1.K = hidden; g1.N = inter;
   g1.n_tiles_n = inter / (Cfg::BN / 2);
@@ -1151,10 +1158,11 @@ int run_gate_up(const void* x, int64_t n_tokens, int top_k, const int32_t* perm,
 
 template <int DT, class Cfg>
 int run_down(const void* act, int top_k, const int32_t* perm, const int32_t* offsets, int n_local,
-             int64_t max_rows, const void* w_out, int hidden, int inter, void* y, int32_t* tile_queue,
-             hipStream_t stream) {
+             int64_t max_rows, const void* w_out, const int32_t* w_slot, int hidden, int inter, void* y,
+             int32_t* tile_queue, hipStream_t stream) {
   GemmParams g2;
   g2.A = act; g2.perm = perm; g2.offsets = offsets; g2.W = w_out; g2.C = y; g2.tile_queue = tile_queue;
+  g2.w_slot = w_slot;
   g2.w_expert_stride = static_cast<int64_t>(hidden) * inter;
   g2.n_local = n_local; g2.top_k = top_k; g2.K = inter; g2.N = hidden;
   g2.n_tiles_n = hidden / Cfg::BN;
@@ -1196,28 +1204,76 @@ bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0;
 using namespace mep;
 
 
+namespace mep {
+namespace {
+
+int gate_up_impl(const char* fn, const void* x, int64_t n_tokens, int32_t top_k, const int32_t* perm,
+                 const int32_t* offsets, int32_t n_local, int64_t max_rows, const void* w_in,
+                 const int32_t* w_slot, int32_t hidden, int32_t inter, int32_t dtype, void* act,
+                 size_t act_bytes, int32_t* tile_queue, void* stream) {
+  int rc = check_expert_args(fn, n_tokens, top_k, n_local, max_rows, hidden, inter, dtype);
+  if (rc != MEP_OK) return rc;
+  if (max_rows == 0 || n_local == 0) return MEP_OK;
+  MEP_REQUIRE(x && perm && offsets && w_in && act && tile_queue, MEP_ERR_INVALID_ARG, "%s: null pointer", fn);
+  const size_t need = static_cast<size_t>(max_rows) * inter * dtype_bytes(dtype);
+  MEP_REQUIRE(act_bytes >= need, MEP_ERR_WORKSPACE, "%s: act %zu B < required %zu B", fn, act_bytes, need);
+  MEP_REQUIRE(aligned16(x) && aligned16(w_in) && aligned16(act), MEP_ERR_INVALID_ARG,
+              "%s: buffers must be 16-byte aligned", fn);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == MEP_DTYPE_BF16)
+    return run_gate_up<MEP_DTYPE_BF16, CfgBf16>(x, n_tokens, top_k, perm, offsets, n_local, max_rows, w_in, w_slot,
+                                                hidden, inter, act, tile_queue, s);
+  return run_gate_up<MEP_DTYPE_F32, CfgF32>(x, n_tokens, top_k, perm, offsets, n_local, max_rows, w_in, w_slot,
+                                            hidden, inter, act, tile_queue, s);
+}
+
+int down_impl(const char* fn, const void* act, int64_t n_tokens, int32_t top_k, const int32_t* perm,
+              const int32_t* offsets, int32_t n_local, int64_t max_rows, const void* w_out, const int32_t* w_slot,
+              int32_t hidden, int32_t inter, int32_t dtype, void* y_entries, int32_t* tile_queue, void* stream) {
+  int rc = check_expert_args(fn, n_tokens, top_k, n_local, max_rows, hidden, inter, dtype);
+  if (rc != MEP_OK) return rc;
+  if (max_rows == 0 || n_local == 0) return MEP_OK;
+  MEP_REQUIRE(act && perm && offsets && w_out && y_entries && tile_queue, MEP_ERR_INVALID_ARG,
+              "%s: null pointer", fn);
+  MEP_REQUIRE(aligned16(act) && aligned16(w_out) && aligned16(y_entries), MEP_ERR_INVALID_ARG,
+              "%s: buffers must be 16-byte aligned", fn);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == MEP_DTYPE_BF16)
+    return run_down<MEP_DTYPE_BF16, CfgBf16>(act, top_k, perm, offsets, n_local, max_rows, w_out, w_slot, hidden,
+                                             inter, y_entries, tile_queue, s);
+  return run_down<MEP_DTYPE_F32, CfgF32>(act, top_k, perm, offsets, n_local, max_rows, w_out, w_slot, hidden,
+                                         inter, y_entries, tile_queue, s);
+}
+
+int grouped_impl(const char* fn, const void* x, int64_t n_tokens, int32_t top_k, const int32_t* perm,
+                 const int32_t* offsets, int32_t n_local, int64_t max_rows, const void* w_in, const void* w_out,
+                 const int32_t* w_slot, int32_t hidden, int32_t inter, int32_t dtype, void* y_entries,
+                 void* workspace, size_t workspace_bytes, int32_t* tile_queue, void* stream) {
+  int rc = check_expert_args(fn, n_tokens, top_k, n_local, max_rows, hidden, inter, dtype);
+  if (rc != MEP_OK) return rc;
+  if (max_rows == 0 || n_local == 0) return MEP_OK;
+  MEP_REQUIRE(workspace != nullptr, MEP_ERR_INVALID_ARG, "%s: null workspace", fn);
+  const size_t need = mep_experts_workspace_size(max_rows, inter, dtype);
+  MEP_REQUIRE(workspace_bytes >= need, MEP_ERR_WORKSPACE, "%s: workspace %zu B < required %zu B", fn,
+              workspace_bytes, need);
+  rc = gate_up_impl(fn, x, n_tokens, top_k, perm, offsets, n_local, max_rows, w_in, w_slot, hidden, inter, dtype,
+                    workspace, workspace_bytes, tile_queue, stream);
+  if (rc != MEP_OK) return rc;
+  return down_impl(fn, workspace, n_tokens, top_k, perm, offsets, n_local, max_rows, w_out, w_slot, hidden, inter,
+                   dtype, y_entries, tile_queue, stream);
+}
+
+}  // namespace
+}  // namespace mep
+
 extern "C" int mep_swiglu_gate_up(const void* x, int64_t n_tokens, int32_t top_k,
                                   const int32_t* perm, const int32_t* offsets, int32_t n_local,
                                   int64_t max_rows, const void* w_in, int32_t hidden, int32_t inter,
                                   int32_t dtype, void* act, size_t act_bytes, int32_t* tile_queue,
                                   void* stream) {
   clear_error();
-  int rc = check_expert_args("mep_swiglu_gate_up", n_tokens, top_k, n_local, max_rows, hidden, inter, dtype);
-  if (rc != MEP_OK) return rc;
-  if (max_rows == 0 || n_local == 0) return MEP_OK;
-  MEP_REQUIRE(x && perm && offsets && w_in && act && tile_queue, MEP_ERR_INVALID_ARG,
-              "mep_swiglu_gate_up: null pointer");
-  const size_t need = static_cast<size_t>(max_rows) * inter * dtype_bytes(dtype);
-  MEP_REQUIRE(act_bytes >= need, MEP_ERR_WORKSPACE, "mep_swiglu_gate_up: act %zu B < required %zu B",
-              act_bytes, need);
-  MEP_REQUIRE(aligned16(x) && aligned16(w_in) && aligned16(act), MEP_ERR_INVALID_ARG,
-              "mep_swiglu_gate_up: buffers must be 16-byte aligned");
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  if (dtype == MEP_DTYPE_BF16)
-    return run_gate_up<MEP_DTYPE_BF16, CfgBf16>(x, n_tokens, top_k, perm, offsets, n_local, max_rows, w_in,
-                                                hidden, inter, act, tile_queue, s);
-  return run_gate_up<MEP_DTYPE_F32, CfgF32>(x, n_tokens, top_k, perm, offsets, n_local, max_rows, w_in, hidden,
-                                            inter, act, tile_queue, s);
+  return gate_up_impl("mep_swiglu_gate_up", x, n_tokens, top_k, perm, offsets, n_local, max_rows, w_in, nullptr,
+                      hidden, inter, dtype, act, act_bytes, tile_queue, stream);
 }
 
 extern "C" int mep_swiglu_down(const void* act, int64_t n_tokens, int32_t top_k, const int32_t* perm,
@@ -1225,19 +1281,8 @@ extern "C" int mep_swiglu_down(const void* act, int64_t n_tokens, int32_t top_k,
                                const void* w_out, int32_t hidden, int32_t inter, int32_t dtype,
                                void* y_entries, int32_t* tile_queue, void* stream) {
   clear_error();
-  int rc = check_expert_args("mep_swiglu_down", n_tokens, top_k, n_local, max_rows, hidden, inter, dtype);
-  if (rc != MEP_OK) return rc;
-  if (max_rows == 0 || n_local == 0) return MEP_OK;
-  MEP_REQUIRE(act && perm && offsets && w_out && y_entries && tile_queue, MEP_ERR_INVALID_ARG,
-              "mep_swiglu_down: null pointer");
-  MEP_REQUIRE(aligned16(act) && aligned16(w_out) && aligned16(y_entries), MEP_ERR_INVALID_ARG,
-              "mep_swiglu_down: buffers must be 16-byte aligned");
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  if (dtype == MEP_DTYPE_BF16)
-    return run_down<MEP_DTYPE_BF16, CfgBf16>(act, top_k, perm, offsets, n_local, max_rows, w_out, hidden,
-                                             inter, y_entries, tile_queue, s);
-  return run_down<MEP_DTYPE_F32, CfgF32>(act, top_k, perm, offsets, n_local, max_rows, w_out, hidden, inter,
-                                         y_entries, tile_queue, s);
+  return down_impl("mep_swiglu_down", act, n_tokens, top_k, perm, offsets, n_local, max_rows, w_out, nullptr,
+                   hidden, inter, dtype, y_entries, tile_queue, stream);
 }
 
 extern "C" size_t mep_experts_workspace_size(int64_t max_rows, int32_t inter, int32_t dtype) {
@@ -1253,16 +1298,20 @@ extern "C" int mep_grouped_swiglu(const void* x, int64_t n_tokens, int32_t top_k
                                   void* workspace, size_t workspace_bytes, int32_t* tile_queue,
                                   void* stream) {
   clear_error();
-  int rc = check_expert_args("mep_grouped_swiglu", n_tokens, top_k, n_local, max_rows, hidden, inter, dtype);
-  if (rc != MEP_OK) return rc;
-  if (max_rows == 0 || n_local == 0) return MEP_OK;
-  MEP_REQUIRE(workspace != nullptr, MEP_ERR_INVALID_ARG, "mep_grouped_swiglu: null workspace");
-  const size_t need = mep_experts_workspace_size(max_rows, inter, dtype);
-  MEP_REQUIRE(workspace_bytes >= need, MEP_ERR_WORKSPACE,
-              "mep_grouped_swiglu: workspace %zu B < required %zu B", workspace_bytes, need);
-  rc = mep_swiglu_gate_up(x, n_tokens, top_k, perm, offsets, n_local, max_rows, w_in, hidden, inter, dtype,
-                          workspace, workspace_bytes, tile_queue, stream);
-  if (rc != MEP_OK) return rc;
-  return mep_swiglu_down(workspace, n_tokens, top_k, perm, offsets, n_local, max_rows, w_out, hidden, inter,
-                         dtype, y_entries, tile_queue, stream);
+  return grouped_impl("mep_grouped_swiglu", x, n_tokens, top_k, perm, offsets, n_local, max_rows, w_in, w_out,
+                      nullptr, hidden, inter, dtype, y_entries, workspace, workspace_bytes, tile_queue, stream);
+}
+
+extern "C" int mep_grouped_swiglu_slots(const void* x, int64_t n_tokens, int32_t top_k,
+                                        const int32_t* perm, const int32_t* offsets, int32_t n_local,
+                                        int64_t max_rows, const void* w_in, const void* w_out,
+                                        const int32_t* w_slot, int32_t hidden, int32_t inter, int32_t dtype,
+                                        void* y_entries, void* workspace, size_t workspace_bytes,
+                                        int32_t* tile_queue, void* stream) {
+  clear_error();
+  MEP_REQUIRE(w_slot != nullptr || n_local == 0 || max_rows == 0, MEP_ERR_INVALID_ARG,
+              "mep_grouped_swiglu_slots: null w_slot");
+  return grouped_impl("mep_grouped_swiglu_slots", x, n_tokens, top_k, perm, offsets, n_local, max_rows, w_in,
+                      w_out, w_slot, hidden, inter, dtype, y_entries, workspace, workspace_bytes, tile_queue,
+                      stream);
 }

@@ -6,6 +6,7 @@ miniep/ep.py, miniep/balancer.py) over the C ABI of ``include/miniep_amd.h``:
   route / HipMoEBackend / HipEPShareBackend / EmulatedEPMoEBackend / EPStats
   Placement (naive / from_plan / to_plan / experts_of_rank / reset_rr / dest_ranks)
   plan_balanced
+  ExpertStore / apply_placement (expert weights in slots, live re-placement)
   ops: router_topk, topk_softmax, dispatch, grouped_swiglu, combine
 """
 from . import _lib, ops
@@ -13,9 +14,10 @@ from .backend import (EmulatedEPExchangeBackend, EmulatedEPMoEBackend, EPStats, 
                       HipMoEBackend, SendBatch, route)
 from .balancer import plan_balanced
 from .placement import Placement
+from .store import ExpertStore, apply_placement
 
 __all__ = [
     "EmulatedEPExchangeBackend", "SendBatch",
     "_lib", "ops", "route", "HipMoEBackend", "HipEPShareBackend", "EmulatedEPMoEBackend",
-    "EPStats", "Placement", "plan_balanced",
+    "EPStats", "Placement", "plan_balanced", "ExpertStore", "apply_placement",
 ]

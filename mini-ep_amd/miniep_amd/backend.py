@@ -99,20 +99,27 @@ class HipEPShareBackend:
     local weights and written to their (token, slot) cell of ``y_entries``.
     """
 
-    def __init__(self, layer: int, placement: Placement, my_rank: int, w_in: torch.Tensor,
-                 w_out: torch.Tensor, stats: EPStats | None = None, check: bool = True):
+    def __init__(self, layer: int, placement: Placement, my_rank: int, w_in: torch.Tensor | None = None,
+                 w_out: torch.Tensor | None = None, stats: EPStats | None = None, check: bool = True,
+                 store=None):
         self.layer = layer
         self.placement = placement
         self.my_rank = my_rank
-        self.w_in = w_in.contiguous()
-        self.w_out = w_out.contiguous()
         self.stats = stats
         self.check = check
-        self._update_map(placement.experts_of_rank(my_rank)[layer])
+        self.w_slot = None
+        if store is not None:
+            self.use_store(placement, store)
+        else:
+            if w_in is None or w_out is None:
+                raise ValueError("give the rank's expert weights or an ExpertStore")
+            self.w_in = w_in.contiguous()
+            self.w_out = w_out.contiguous()
+            self._update_map(placement.experts_of_rank(my_rank)[layer])
 
     def _update_map(self, local_experts: list[int]):
         """g2l: global -> local expert id, -1 if not resident (ep.py:203-208)."""
-        if len(local_experts) != self.w_in.shape[0]:
+        if self.w_slot is None and len(local_experts) != self.w_in.shape[0]:
             raise ValueError(f"{len(local_experts)} local experts but w_in holds {self.w_in.shape[0]}")
         self.local_experts = list(local_experts)
         g2l = torch.full((self.placement.num_experts,), -1, dtype=torch.int32)
@@ -125,7 +132,19 @@ class HipEPShareBackend:
         (the hot swap of server.py:51-62)."""
         self.placement = placement
         self.w_in, self.w_out = w_in.contiguous(), w_out.contiguous()
+        self.w_slot = None
         self._update_map(placement.experts_of_rank(self.my_rank)[self.layer])
+
+    def use_store(self, placement: Placement, store) -> None:
+        """Read this layer's experts from an ExpertStore's slots (whose resident
+        set must be the placement's experts of this rank)."""
+        local = placement.experts_of_rank(self.my_rank)[self.layer]
+        if store.local_experts[self.layer] != local:
+            raise ValueError(f"layer {self.layer}: the store holds {store.local_experts[self.layer]}, "
+                             f"the placement gives rank {self.my_rank} {local}")
+        self.placement = placement
+        self.w_in, self.w_out, self.w_slot = store.layer_weights(self.layer)
+        self._update_map(local)
 
     def dispatch(self, topk_idx, valid_mask=None, seg_tokens=None, rr=None, want_dest=False):
         n = topk_idx.shape[0]
@@ -184,13 +203,14 @@ class HipEPShareBackend:
                          len(self.local_experts), check=self.check)
         if self.stats is not None:
             self.stats.recv_tokens_per_layer[self.layer] += d.offsets[-1].to(torch.long)
-        return ops.grouped_swiglu(recv_x.to(self.w_in.dtype), d, self.w_in, self.w_out)
+        return ops.grouped_swiglu(recv_x.to(self.w_in.dtype), d, self.w_in, self.w_out, w_slot=self.w_slot)
 
     def share(self, x_flat, topk_idx, valid_mask=None, seg_tokens=None, rr=None, y_entries=None,
               want_dest=False):
         """(Dispatch, y_entries): this rank's rows and their expert outputs."""
         disp = self.dispatch(topk_idx, valid_mask, seg_tokens, rr, want_dest)
-        y = ops.grouped_swiglu(x_flat.to(self.w_in.dtype), disp, self.w_in, self.w_out, y_entries)
+        y = ops.grouped_swiglu(x_flat.to(self.w_in.dtype), disp, self.w_in, self.w_out, y_entries,
+                               w_slot=self.w_slot)
         return disp, y
 
 
@@ -257,11 +277,18 @@ class EmulatedEPMoEBackend:
     every share writes the common (token, slot) buffer, then one combine in
     canonical slot order.  Equal to HipMoEBackend bit for bit for any
     placement, which is the reference's placement-invariance property
-    (ep.py:1-8)."""
+    (ep.py:1-8).  With ``stores`` (one ExpertStore per rank, holding that
+    rank's experts of the placement) the ranks read their weights from the
+    stores' slots instead of slices of the full weights."""
 
-    def __init__(self, layer: int, placement: Placement, world: int, w_in_full: torch.Tensor,
-                 w_out_full: torch.Tensor, check: bool = True):
+    def __init__(self, layer: int, placement: Placement, world: int, w_in_full: torch.Tensor | None = None,
+                 w_out_full: torch.Tensor | None = None, check: bool = True, stores=None):
         self.layer, self.placement, self.world = layer, placement, world
+        if stores is not None:
+            # each rank reads its experts from its own ExpertStore's slots
+            self.ranks = [HipEPShareBackend(layer, placement, r, check=check, store=stores[r])
+                          for r in range(world)]
+            return
         mine = [placement.experts_of_rank(r)[layer] for r in range(world)]
         self.ranks = [HipEPShareBackend(layer, placement, r, w_in_full[ids], w_out_full[ids],
                                         check=check) for r, ids in enumerate(mine)]

@@ -184,17 +184,22 @@ def dispatch(topk_idx: torch.Tensor, valid_mask: torch.Tensor | None, n_experts:
 # grouped SwiGLU experts (modeling.py:83-104) and combine (modeling.py:120-128,144)
 # ----------------------------------------------------------------------------
 def grouped_swiglu(x_flat: torch.Tensor, disp: Dispatch, w_in: torch.Tensor, w_out: torch.Tensor,
-                   y_entries: torch.Tensor | None = None) -> torch.Tensor:
+                   y_entries: torch.Tensor | None = None, w_slot: torch.Tensor | None = None) -> torch.Tensor:
     """Expert outputs for every dispatched row, written to the row's
-    (token, slot) cell of ``y_entries`` (N*k, H) (allocated if not given)."""
-    dev = _require_device(x_flat, w_in, w_out, y_entries)
+    (token, slot) cell of ``y_entries`` (N*k, H) (allocated if not given).
+    With ``w_slot`` (n_local,) int32, local expert j's weights are slot
+    w_slot[j] of w_in (n_slots, 2I, H) / w_out (n_slots, H, I)."""
+    dev = _require_device(x_flat, w_in, w_out, y_entries, w_slot)
     x = x_flat.contiguous()
     n, h = x.shape
     if w_in.dim() != 3 or w_out.dim() != 3:
         raise ValueError("w_in must be (E, 2I, H) and w_out (E, H, I)")
     e_loc, two_i, h_in = w_in.shape
     inter = two_i // 2
-    if h_in != h or tuple(w_out.shape) != (e_loc, h, inter) or e_loc != disp.n_local:
+    n_w = disp.n_local if w_slot is None else e_loc
+    if w_slot is not None and (w_slot.dtype != torch.int32 or w_slot.numel() != disp.n_local):
+        raise ValueError(f"w_slot must hold {disp.n_local} int32 slots")
+    if h_in != h or tuple(w_out.shape) != (e_loc, h, inter) or e_loc != n_w:
         raise ValueError(f"weight shapes {tuple(w_in.shape)} / {tuple(w_out.shape)} do not match "
                          f"hidden {h} and {disp.n_local} local experts")
     wi = w_in.to(x.dtype).contiguous()
@@ -206,12 +211,43 @@ def grouped_swiglu(x_flat: torch.Tensor, disp: Dispatch, w_in: torch.Tensor, w_o
     max_rows = n * disp.top_k
     ws_bytes = L.mep_experts_workspace_size(max_rows, inter, code)
     ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
-    rc = L.mep_grouped_swiglu(x.data_ptr(), n, disp.top_k, disp.perm.data_ptr(), disp.offsets.data_ptr(),
-                              disp.n_local, max_rows, wi.data_ptr(), wo.data_ptr(), h, inter, code,
-                              y_entries.data_ptr(), ws.data_ptr(), ws.numel(), _tile_queue(dev).data_ptr(),
-                              _stream(dev))
-    _lib.check(rc, "mep_grouped_swiglu")
+    if w_slot is None:
+        rc = L.mep_grouped_swiglu(x.data_ptr(), n, disp.top_k, disp.perm.data_ptr(), disp.offsets.data_ptr(),
+                                  disp.n_local, max_rows, wi.data_ptr(), wo.data_ptr(), h, inter, code,
+                                  y_entries.data_ptr(), ws.data_ptr(), ws.numel(), _tile_queue(dev).data_ptr(),
+                                  _stream(dev))
+        _lib.check(rc, "mep_grouped_swiglu")
+    else:
+        rc = L.mep_grouped_swiglu_slots(x.data_ptr(), n, disp.top_k, disp.perm.data_ptr(),
+                                        disp.offsets.data_ptr(), disp.n_local, max_rows, wi.data_ptr(),
+                                        wo.data_ptr(), w_slot.contiguous().data_ptr(), h, inter, code,
+                                        y_entries.data_ptr(), ws.data_ptr(), ws.numel(),
+                                        _tile_queue(dev).data_ptr(), _stream(dev))
+        _lib.check(rc, "mep_grouped_swiglu_slots")
     return y_entries
+
+
+def copy_experts(src_in: torch.Tensor, src_out: torch.Tensor, src_index: list[int], dst_in: torch.Tensor,
+                 dst_out: torch.Tensor, dst_slot: list[int]) -> None:
+    """Slot dst_slot[i] of (dst_in, dst_out) = expert src_index[i] of
+    (src_in, src_out), one launch (mep_copy_experts); all four are device
+    tensors in the checkpoint layout (E, 2I, H) / (E, H, I)."""
+    dev = _require_device(src_in, src_out, dst_in, dst_out)
+    n = len(src_index)
+    if n != len(dst_slot):
+        raise ValueError("src_index and dst_slot differ in length")
+    if n == 0:
+        return
+    for t in (src_in, src_out, dst_in, dst_out):
+        if not t.is_contiguous() or t.dtype != dst_in.dtype:
+            raise TypeError("expert tensors must be contiguous and of one dtype")
+    e_src, two_i, h = src_in.shape
+    arr_s = (ctypes.c_int32 * n)(*[int(v) for v in src_index])
+    arr_d = (ctypes.c_int32 * n)(*[int(v) for v in dst_slot])
+    rc = _lib.lib().mep_copy_experts(src_in.data_ptr(), src_out.data_ptr(), e_src, dst_in.data_ptr(),
+                                     dst_out.data_ptr(), dst_in.shape[0], arr_s, arr_d, n, h, two_i // 2,
+                                     _dtype_code(dst_in), _stream(dev))
+    _lib.check(rc, "mep_copy_experts")
 
 
 def _expert_shapes(x, disp, w_in=None, w_out=None):
