@@ -162,6 +162,26 @@ int mep_dispatch_noalloc(const int64_t* topk_idx, const uint8_t* valid_mask, int
                          uint32_t* status, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Router + dispatch of the all-local backend, fused: mep_router_topk
+ * followed by mep_dispatch with one segment and every expert on this GPU
+ * (LocalMoEBackend: table 0, n_rep 1, g2l identity, n_local = E), the
+ * modeling.py:193-196 router feeding modeling.py:94-96,107-117.  The router
+ * kernel also counts each 64-token workgroup's entries per expert, which for
+ * top_k = 8 is the dispatch's per-block histogram, so the dispatch runs one
+ * launch fewer.  Outputs and the workspace check (mep_dispatch_check) are
+ * those of the two calls, bit for bit; route_counts (E,) int64 or NULL:
+ * += per-expert valid-entry counts.  Supported: top_k = 8, E in {16, 32, 64},
+ * H % 256 == 0; other shapes use the two calls.
+ * ---------------------------------------------------------------------- */
+size_t mep_route_dispatch_workspace_size(int64_t n_tokens, int32_t n_experts);
+
+int mep_route_dispatch(const void* x, const void* w_router, const uint8_t* valid_mask, int64_t n_tokens,
+                       int32_t hidden, int32_t n_experts, int32_t top_k, int32_t dtype,
+                       int64_t* topk_idx, void* topk_gate, float* logits,
+                       int32_t* counts, int32_t* offsets, int32_t* perm, int32_t* row_of_entry,
+                       int64_t* route_counts, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
  * Grouped SwiGLU experts over the dispatched rows (run_experts,
  * modeling.py:83-104), fused with the row gather (modeling.py:143) and the
  * scatter back to entry order:

@@ -59,6 +59,15 @@ void set_error(const char* fmt, ...);
 void clear_error();
 // compute units of the current device (cached per device)
 int device_cu_count();
+// The router kernel with its histogram output (router.hip): per 64-token
+// workgroup b, bc[b * E + e] = entries of expert e among its valid tokens;
+// it also writes the dispatch workspace's header[0] = n_blocks, flags[b] = 0
+// and the world-1 tables (table 0, n_rep 1, g2l identity) into tables[3E].
+// top_k must be 8.
+hipError_t launch_router_with_hist(const void* x, const void* w, int64_t n, int hidden, int E, int k, int dtype,
+                                   int64_t* idx, void* gate, float* logits, int32_t* bc, uint32_t* header,
+                                   uint32_t* flags, int32_t* tables, const uint8_t* valid, int n_blocks,
+                                   hipStream_t stream);
 
 inline int dtype_bytes(int dtype) {
   return dtype == MEP_DTYPE_F32 ? 4 : (dtype == MEP_DTYPE_BF16 ? 2 : 0);

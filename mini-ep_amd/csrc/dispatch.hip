@@ -559,6 +559,113 @@ extern "C" int mep_dispatch_noalloc(const int64_t* topk_idx, const uint8_t* vali
                        perm, row_of_entry, dest, route_counts, status, nullptr, 0, stream);
 }
 
+namespace mep {
+namespace {
+
+// Dispatch result of an empty batch: no rows, and a workspace that
+// mep_dispatch_check reads as one block without flags.
+__global__ void empty_route_kernel(int n_local, int32_t* counts, int32_t* offsets, uint32_t* header,
+                                   uint32_t* flags) {
+  for (int j = threadIdx.x; j <= n_local; j += blockDim.x) {
+    offsets[j] = 0;
+    if (j < n_local) counts[j] = 0;
+  }
+  if (threadIdx.x == 0) {
+    header[0] = 1u;
+    flags[0] = 0u;
+    flags[1] = 0u;
+  }
+}
+
+size_t route_tables_offset(const WsLayout& l) { return l.total; }
+
+WsLayout route_layout(int64_t n_tokens, int32_t n_experts, int* nb_out) {
+  const int nb = static_cast<int>((n_tokens * 8 + kChunk - 1) / kChunk);
+  *nb_out = nb;
+  return ws_layout(nb > 0 ? nb : 1, 1, n_experts);
+}
+
+}  // namespace
+}  // namespace mep
+
+extern "C" size_t mep_route_dispatch_workspace_size(int64_t n_tokens, int32_t n_experts) {
+  if (n_tokens < 0 || n_experts <= 0 || n_experts > kMaxExperts) return 0;
+  int nb = 0;
+  const WsLayout l = route_layout(n_tokens, n_experts, &nb);
+  return route_tables_offset(l) + align_up(sizeof(int32_t) * 3 * n_experts, 256);
+}
+
+extern "C" int mep_route_dispatch(const void* x, const void* w_router, const uint8_t* valid_mask, int64_t n_tokens,
+                                  int32_t hidden, int32_t n_experts, int32_t top_k, int32_t dtype,
+                                  int64_t* topk_idx, void* topk_gate, float* logits, int32_t* counts,
+                                  int32_t* offsets, int32_t* perm, int32_t* row_of_entry, int64_t* route_counts,
+                                  void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  const char* fn = "mep_route_dispatch";
+  MEP_REQUIRE(n_tokens >= 0, MEP_ERR_INVALID_ARG, "%s: n_tokens < 0", fn);
+  MEP_REQUIRE(dtype == MEP_DTYPE_F32 || dtype == MEP_DTYPE_BF16, MEP_ERR_INVALID_ARG, "%s: unknown dtype %d", fn,
+              dtype);
+  MEP_REQUIRE(top_k == 8, MEP_ERR_UNSUPPORTED, "%s: top_k must be 8 (got %d); use mep_router_topk + mep_dispatch",
+              fn, top_k);
+  MEP_REQUIRE(n_experts == 16 || n_experts == 32 || n_experts == 64, MEP_ERR_UNSUPPORTED,
+              "%s: n_experts must be 16, 32 or 64 (got %d)", fn, n_experts);
+  MEP_REQUIRE(hidden > 0 && hidden % 256 == 0, MEP_ERR_UNSUPPORTED,
+              "%s: hidden %d must be a positive multiple of 256", fn, hidden);
+  MEP_REQUIRE(n_tokens * top_k < (int64_t(1) << 31), MEP_ERR_UNSUPPORTED, "%s: n_tokens * top_k must be < 2^31",
+              fn);
+  MEP_REQUIRE(counts && offsets && workspace, MEP_ERR_INVALID_ARG, "%s: null counts / offsets / workspace", fn);
+  MEP_REQUIRE(n_tokens == 0 || (x && w_router && topk_idx && topk_gate && perm && row_of_entry),
+              MEP_ERR_INVALID_ARG, "%s: null pointer", fn);
+  int nb = 0;
+  const WsLayout l = route_layout(n_tokens, n_experts, &nb);
+  const size_t need = mep_route_dispatch_workspace_size(n_tokens, n_experts);
+  MEP_REQUIRE(workspace_bytes >= need, MEP_ERR_WORKSPACE, "%s: workspace %zu B < required %zu B", fn,
+              workspace_bytes, need);
+  char* ws = static_cast<char*>(workspace);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (n_tokens == 0) {
+    empty_route_kernel<<<1, 256, 0, st>>>(n_experts, counts, offsets, reinterpret_cast<uint32_t*>(ws + l.header),
+                                          reinterpret_cast<uint32_t*>(ws + l.flags));
+    MEP_CHECK_LAUNCH("mep_route_dispatch(empty)");
+    return MEP_OK;
+  }
+  int32_t* tables = reinterpret_cast<int32_t*>(ws + route_tables_offset(l));
+  hipError_t e = launch_router_with_hist(x, w_router, n_tokens, hidden, n_experts, top_k, dtype, topk_idx,
+                                         topk_gate, logits, reinterpret_cast<int32_t*>(ws + l.bc),
+                                         reinterpret_cast<uint32_t*>(ws + l.header),
+                                         reinterpret_cast<uint32_t*>(ws + l.flags), tables, valid_mask, nb, st);
+  MEP_REQUIRE(e == hipSuccess, MEP_ERR_HIP, "%s: router launch failed: %s", fn, hipGetErrorString(e));
+
+  DispatchParams p;
+  p.nb = nb;
+  p.nbl = nb;
+  p.seg_block[0] = 0;
+  p.seg_block[1] = nb;
+  p.topk_idx = topk_idx; p.valid = valid_mask; p.n_tokens = n_tokens;
+  p.k = top_k; p.E = n_experts; p.table = tables; p.n_rep = tables + n_experts; p.rmax = 1;
+  p.has_rep = 0; p.rr = nullptr; p.my_rank = 0; p.g2l = tables + 2 * n_experts;
+  p.n_local = n_experts; p.counts = counts; p.offsets = offsets; p.perm = perm;
+  p.row_of_entry = row_of_entry; p.dest = nullptr; p.route_counts = route_counts;
+  p.status = nullptr;
+  p.header = reinterpret_cast<uint32_t*>(ws + l.header);
+  p.flags = reinterpret_cast<uint32_t*>(ws + l.flags);
+  p.rr_snap = reinterpret_cast<int64_t*>(ws + l.rr_snap);
+  p.bc = reinterpret_cast<int32_t*>(ws + l.bc);
+  p.segtot = reinterpret_cast<int32_t*>(ws + l.segtot);
+  p.scanned = p.nb > kScanBlocks ? 1 : 0;
+  p.n_seg = 1;
+  p.seg_entry[0] = 0;
+  for (int s = 1; s <= kMaxSeg; ++s) p.seg_entry[s] = n_tokens * top_k;
+  for (int s = 2; s <= kMaxSeg; ++s) p.seg_block[s] = p.nb;
+  if (p.scanned) {
+    prefix_kernel<<<n_experts, kScanThreads, 0, st>>>(p);
+    MEP_CHECK_LAUNCH("mep_route_dispatch(prefix)");
+  }
+  scatter_kernel<<<p.nbl, kThreads, 0, st>>>(p);
+  MEP_CHECK_LAUNCH("mep_route_dispatch(scatter)");
+  return MEP_OK;
+}
+
 extern "C" int mep_dispatch_check(const void* workspace, void* stream) {
   clear_error();
   MEP_REQUIRE(workspace != nullptr, MEP_ERR_INVALID_ARG, "mep_dispatch_check: null workspace");

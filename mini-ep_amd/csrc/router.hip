@@ -10,12 +10,16 @@
 // v_mfma_f32_16x16x32_bf16, fp32: v_mfma_f32_16x16x4_f32) with fp32
 // accumulation; each wave issues all loads of its x rows for a K segment
 // before its first MFMA, so HBM latency is paid once per segment.
-// The tile then goes to LDS and every (token, expert) pair gets its rank
-//     rank(e) = #{e' : key(e') > key(e)  or  (key(e') == key(e) and e' < e)}
-// which is a total order: descending logits, lower expert id first among
-// equal logits (NaN ranks above every number, -0.0 == +0.0).  Pairs with
-// rank < k land directly in output slot `rank`; no sort, no atomics, so the
-// selection is deterministic and independent of the launch shape.
+// The selection orders (token, expert) pairs by the total order
+//     e' before e  <=>  key(e') > key(e)  or  (key(e') == key(e) and e' < e)
+// (descending logits, lower expert id first among equal logits, NaN above
+// every number, -0.0 == +0.0).  For 32 experts and top-8 the four lanes of a
+// token sort their 8 keys each and merge them with sorting networks in
+// registers; other shapes rank every pair (rank(e) = #{e' before e}) and put
+// rank < k in output slot `rank`.  No atomics decide anything, so the
+// selection is deterministic and independent of the launch shape.  With the
+// dispatch histogram output (mep_route_dispatch) each workgroup also counts
+// the entries per expert of its 64 tokens.
 #include "common.h"
 
 namespace mep {
@@ -123,70 +127,173 @@ __device__ void select_topk_from_lds(const float* lg, int ld, int rows, int E_rt
   }
 }
 
+// Float of a total-order key (inverse of order_key; -0.0 comes back as +0.0,
+// NaN as NaN).
+__device__ __forceinline__ float key_value(uint64_t key) {
+  const uint32_t u = static_cast<uint32_t>(key >> 32);
+  return __uint_as_float((u & 0x80000000u) ? (u & 0x7fffffffu) : ~u);
+}
+
+// Descending compare-exchange of two keys.
+__device__ __forceinline__ void cx_desc(uint64_t& a, uint64_t& b) {
+  const bool keep = a > b;
+  const uint64_t hi = keep ? a : b, lo = keep ? b : a;
+  a = hi;
+  b = lo;
+}
+
+// The key of the lane XOR 1 or XOR 2 within this lane's group of four
+// (DPP quad_perm [1,0,3,2] / [2,3,0,1]).
+template <int CTRL>
+__device__ __forceinline__ uint64_t quad_swap(uint64_t v) {
+  const int lo = __builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<uint32_t>(v)), CTRL, 0xF, 0xF, false);
+  const int hi = __builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<uint32_t>(v >> 32)), CTRL, 0xF, 0xF,
+                                             false);
+  return (static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) | static_cast<uint32_t>(lo);
+}
+
+// k[0..7] sorted descending, the four lanes of a token each holding 8 of its
+// 32 keys: every lane sorts its 8 (Batcher's 19-comparator network), then
+// takes the top 8 of its list and the partner lane's twice (partner = lane
+// XOR 1, then XOR 2): c[i] = max(a[i], b[7-i]) is the top 8 of the 16 as a
+// bitonic sequence, and a 12-comparator bitonic merge sorts it.  All four
+// lanes end with the token's top 8 in order (keys are distinct).
+__device__ __forceinline__ void top8_of_32(uint64_t (&k)[8]) {
+  cx_desc(k[0], k[2]); cx_desc(k[1], k[3]); cx_desc(k[4], k[6]); cx_desc(k[5], k[7]);
+  cx_desc(k[0], k[4]); cx_desc(k[1], k[5]); cx_desc(k[2], k[6]); cx_desc(k[3], k[7]);
+  cx_desc(k[0], k[1]); cx_desc(k[2], k[3]); cx_desc(k[4], k[5]); cx_desc(k[6], k[7]);
+  cx_desc(k[2], k[4]); cx_desc(k[3], k[5]);
+  cx_desc(k[1], k[4]); cx_desc(k[3], k[6]);
+  cx_desc(k[1], k[2]); cx_desc(k[3], k[4]); cx_desc(k[5], k[6]);
+#pragma unroll
+  for (int level = 0; level < 2; ++level) {
+    uint64_t o[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = level == 0 ? quad_swap<0xB1>(k[i]) : quad_swap<0x4E>(k[i]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) k[i] = k[i] > o[7 - i] ? k[i] : o[7 - i];
+    cx_desc(k[0], k[4]); cx_desc(k[1], k[5]); cx_desc(k[2], k[6]); cx_desc(k[3], k[7]);
+    cx_desc(k[0], k[2]); cx_desc(k[1], k[3]); cx_desc(k[4], k[6]); cx_desc(k[5], k[7]);
+    cx_desc(k[0], k[1]); cx_desc(k[2], k[3]); cx_desc(k[4], k[5]); cx_desc(k[6], k[7]);
+  }
+}
+
+// Optional histogram output of the router (the fused route + dispatch path):
+// per workgroup of 64 tokens, entries of each expert among its valid tokens,
+// which is the dispatch's per-block histogram when top_k = 8 (64 tokens x 8
+// slots = one 512-entry dispatch block).
+struct RouterHist {
+  int32_t* bc;              // (n_blocks, E) histograms, or NULL: no histogram
+  uint32_t* header;         // dispatch workspace header: [0] = n_blocks
+  uint32_t* flags;          // the dispatch's per-block count flags (written 0)
+  int32_t* tables;          // table (E) = 0, n_rep (E) = 1, g2l (E) = identity
+  const uint8_t* valid;     // (N,) or NULL
+  int n_blocks;
+};
+
 // Top-KC of a 16 x EC tile (compile-time EC and KC, both multiples of 4) by
 // one wave, with no workgroup barrier: lane 4 t + g owns token t and experts
-// g*EC/4 .. (g+1)*EC/4 - 1.  Each lane writes its experts' 64-bit keys
-// (order_key << 32 | ~e, as in select_topk_from_lds) to the wave's LDS rows,
-// reads its token's whole row once, and ranks its own experts against it;
-// rank < KC goes to slot `rank`.  Then lane (t, g) writes slots
+// g*EC/4 .. (g+1)*EC/4 - 1.  Every key is the 64-bit (order_key << 32 | ~e)
+// of select_topk_from_lds: unique per expert and ordered exactly as "larger
+// logit first, lower id among equals".  EC = 32, KC = 8: sorting networks in
+// registers (top8_of_32).  Otherwise each lane writes its experts' keys to the
+// wave's LDS rows, reads its token's whole row once and ranks its own experts
+// against it; rank < KC goes to slot `rank`.  Then lane (t, g) writes slots
 // g*KC/4 .. of token t; the softmax is computed by every lane of the token in
 // the same order (max = slot 0, exp of differences summed in slot order), so
 // the gates equal the general path's bit for bit.  All data is wave-private,
-// so s_waitcnt on LDS orders it.
+// so s_waitcnt on LDS orders it.  With a histogram output, each lane adds
+// its slots' experts of valid tokens to the workgroup's `s_cnt`.
 template <int GATE_DT, int EC, int KC>
 __device__ void select_topk_wave(const float* lg, int ld, int64_t t0, int64_t n_tokens, float* sel_val,
                                  int* sel_idx, int64_t* topk_idx, typename Elem<GATE_DT>::T* gate,
-                                 uint64_t* keys, int kld) {
+                                 uint64_t* keys, int kld, const RouterHist& hist, int* s_cnt) {
   static_assert(EC % 4 == 0 && KC % 4 == 0 && KC <= EC && kRowsPerWave * 4 == 64, "lane layout");
   constexpr int EG = EC / 4, SG = KC / 4;
   const int lane = lane_id();
   const int t = lane >> 2, g = lane & 3;
-  float v[EG];
-  uint64_t ke[EG];
+  int my_idx[SG];
+  float my_gate[SG];
+  if constexpr (EC == 32 && KC == 8) {
+    uint64_t k[8];
 #pragma unroll
-  for (int i = 0; i < EG; ++i) {
-    const int e = g * EG + i;
-    v[i] = lg[t * ld + e];
-    ke[i] = (static_cast<uint64_t>(order_key(v[i])) << 32) | static_cast<uint32_t>(~e);
-    keys[t * kld + e] = ke[i];
-  }
-  __builtin_amdgcn_s_waitcnt(0xC07F);            // lgkmcnt(0): the row is in LDS
-  __builtin_amdgcn_wave_barrier();
-  int rank[EG];
+    for (int i = 0; i < 8; ++i) {
+      const int e = g * 8 + i;
+      k[i] = (static_cast<uint64_t>(order_key(lg[t * ld + e])) << 32) | static_cast<uint32_t>(~e);
+    }
+    top8_of_32(k);
+    float sv[8], ex[8], sum = 0.0f;
 #pragma unroll
-  for (int i = 0; i < EG; ++i) rank[i] = 0;
-  const uint64_t* row = keys + t * kld;
+    for (int q = 0; q < 8; ++q) sv[q] = key_value(k[q]);
 #pragma unroll
-  for (int j2 = 0; j2 < EC / 2; ++j2) {
-    const u32x4 q = *reinterpret_cast<const u32x4*>(row + 2 * j2);
-    const uint64_t a = (static_cast<uint64_t>(q.y) << 32) | q.x;
-    const uint64_t b = (static_cast<uint64_t>(q.w) << 32) | q.z;
+    for (int q = 0; q < 8; ++q) { ex[q] = expf(sv[q] - sv[0]); sum += ex[q]; }
 #pragma unroll
-    for (int i = 0; i < EG; ++i) rank[i] += (a > ke[i]) + (b > ke[i]);
-  }
+    for (int h = 0; h < SG; ++h) {
+      uint64_t kq = k[h];
+      float eq = ex[h];
 #pragma unroll
-  for (int i = 0; i < EG; ++i) {
-    if (rank[i] < KC) {
-      sel_val[t * KC + rank[i]] = v[i];
-      sel_idx[t * KC + rank[i]] = g * EG + i;
+      for (int gg = 1; gg < 4; ++gg)
+        if (g == gg) { kq = k[gg * SG + h]; eq = ex[gg * SG + h]; }
+      my_idx[h] = static_cast<int>(~static_cast<uint32_t>(kq));
+      my_gate[h] = eq / sum;
+    }
+  } else {
+    float v[EG];
+    uint64_t ke[EG];
+#pragma unroll
+    for (int i = 0; i < EG; ++i) {
+      const int e = g * EG + i;
+      v[i] = lg[t * ld + e];
+      ke[i] = (static_cast<uint64_t>(order_key(v[i])) << 32) | static_cast<uint32_t>(~e);
+      keys[t * kld + e] = ke[i];
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);            // lgkmcnt(0): the row is in LDS
+    __builtin_amdgcn_wave_barrier();
+    int rank[EG];
+#pragma unroll
+    for (int i = 0; i < EG; ++i) rank[i] = 0;
+    const uint64_t* row = keys + t * kld;
+#pragma unroll
+    for (int j2 = 0; j2 < EC / 2; ++j2) {
+      const u32x4 q = *reinterpret_cast<const u32x4*>(row + 2 * j2);
+      const uint64_t a = (static_cast<uint64_t>(q.y) << 32) | q.x;
+      const uint64_t b = (static_cast<uint64_t>(q.w) << 32) | q.z;
+#pragma unroll
+      for (int i = 0; i < EG; ++i) rank[i] += (a > ke[i]) + (b > ke[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < EG; ++i) {
+      if (rank[i] < KC) {
+        sel_val[t * KC + rank[i]] = v[i];
+        sel_idx[t * KC + rank[i]] = g * EG + i;
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_wave_barrier();
+    float sv[KC];
+#pragma unroll
+    for (int q = 0; q < KC / 4; ++q) {
+      const f32x4 w4 = *reinterpret_cast<const f32x4*>(sel_val + t * KC + 4 * q);
+      sv[4 * q] = w4.x; sv[4 * q + 1] = w4.y; sv[4 * q + 2] = w4.z; sv[4 * q + 3] = w4.w;
+    }
+    float ex[KC], sum = 0.0f;
+#pragma unroll
+    for (int q = 0; q < KC; ++q) { ex[q] = expf(sv[q] - sv[0]); sum += ex[q]; }
+#pragma unroll
+    for (int h = 0; h < SG; ++h) {
+      my_idx[h] = sel_idx[t * KC + g * SG + h];
+      my_gate[h] = ex[g * SG + h] / sum;
     }
   }
-  __builtin_amdgcn_s_waitcnt(0xC07F);
-  __builtin_amdgcn_wave_barrier();
-  float sv[KC];
-#pragma unroll
-  for (int q = 0; q < KC / 4; ++q) {
-    const f32x4 w4 = *reinterpret_cast<const f32x4*>(sel_val + t * KC + 4 * q);
-    sv[4 * q] = w4.x; sv[4 * q + 1] = w4.y; sv[4 * q + 2] = w4.z; sv[4 * q + 3] = w4.w;
-  }
-  float ex[KC], sum = 0.0f;
-#pragma unroll
-  for (int q = 0; q < KC; ++q) { ex[q] = expf(sv[q] - sv[0]); sum += ex[q]; }
   if (t0 + t < n_tokens) {
 #pragma unroll
-    for (int q = g * SG; q < (g + 1) * SG; ++q) {
-      topk_idx[(t0 + t) * KC + q] = sel_idx[t * KC + q];
-      gate[(t0 + t) * KC + q] = Elem<GATE_DT>::from_f32(ex[q] / sum);
+    for (int h = 0; h < SG; ++h) {
+      topk_idx[(t0 + t) * KC + g * SG + h] = my_idx[h];
+      gate[(t0 + t) * KC + g * SG + h] = Elem<GATE_DT>::from_f32(my_gate[h]);
+    }
+    if (hist.bc != nullptr && (hist.valid == nullptr || hist.valid[t0 + t] != 0)) {
+#pragma unroll
+      for (int h = 0; h < SG; ++h) atomicAdd(&s_cnt[my_idx[h]], 1);
     }
   }
 }
@@ -209,7 +316,7 @@ __global__ __launch_bounds__(kWaves * 64) void router_kernel(const typename Elem
                                                              int64_t n_tokens, int hidden, int k,
                                                              int64_t* __restrict__ topk_idx,
                                                              typename Elem<DT>::T* __restrict__ gate,
-                                                             float* __restrict__ logits) {
+                                                             float* __restrict__ logits, RouterHist hist) {
   typedef typename Elem<DT>::T T;
   constexpr int E = NF * 16;
   constexpr int EB = Elem<DT>::kBytes;
@@ -226,8 +333,10 @@ __global__ __launch_bounds__(kWaves * 64) void router_kernel(const typename Elem
   __shared__ __attribute__((aligned(16))) float sel_val[kWaves][kRowsPerWave * 64];
   __shared__ int sel_idx[kWaves][kRowsPerWave * 64];
   __shared__ float rsum[kWaves][kRowsPerWave];
+  __shared__ int s_cnt[E];                        // histogram output: entries per expert
 
   const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
+  if (tid < E) s_cnt[tid] = 0;                    // published by the first barrier below
   const int r = lane & 15, g = lane >> 4;
   const int64_t t0 = (static_cast<int64_t>(blockIdx.x) * kWaves + wave) * kRowsPerWave;
   int64_t tok = t0 + r;
@@ -311,12 +420,28 @@ __global__ __launch_bounds__(kWaves * 64) void router_kernel(const typename Elem
       if (t0 + t < n_tokens) logits[(t0 + t) * E + (p - t * E)] = lg[wave][t][p - t * E];
     }
   }
-  if constexpr (kWaveSelect)
+  if constexpr (kWaveSelect) {
     select_topk_wave<DT, E, KC>(&lg[wave][0][0], E + 1, t0, n_tokens, sel_val[wave], sel_idx[wave], topk_idx, gate,
-                                keys[wave], E + 2);
-  else
+                                keys[wave], E + 2, hist, s_cnt);
+    if (hist.bc != nullptr) {
+      // the workgroup's histogram is the dispatch's histogram of block b
+      __syncthreads();
+      const int b = blockIdx.x;
+      if (tid < E) hist.bc[static_cast<int64_t>(b) * E + tid] = s_cnt[tid];
+      if (tid == 0) hist.flags[b] = 0u;
+      if (b == 0) {
+        if (tid == 0) hist.header[0] = static_cast<uint32_t>(hist.n_blocks);
+        if (tid < E) {
+          hist.tables[tid] = 0;                    // table[e, 0]: every expert on rank 0
+          hist.tables[E + tid] = 1;                // n_rep[e]
+          hist.tables[2 * E + tid] = tid;          // g2l: identity
+        }
+      }
+    }
+  } else {
     select_topk_from_lds<DT, E, KC>(&lg[wave][0][0], E + 1, kRowsPerWave, E, k, t0, n_tokens, sel_val[wave],
                                     sel_idx[wave], rsum[wave], topk_idx, gate, keys[wave], E + 2);
+  }
 }
 
 // Top-k + softmax of precomputed logits: one wave per `rows` tokens.
@@ -344,7 +469,7 @@ __global__ __launch_bounds__(64) void topk_softmax_kernel(const float* __restric
 
 template <int DT>
 hipError_t launch_router(const void* x, const void* w, int64_t n, int hidden, int E, int k,
-                         int64_t* idx, void* gate, float* logits, hipStream_t stream) {
+                         int64_t* idx, void* gate, float* logits, const RouterHist& hist, hipStream_t stream) {
   typedef typename Elem<DT>::T T;
   const int per_block = kWaves * kRowsPerWave;
   const dim3 grid(static_cast<unsigned>((n + per_block - 1) / per_block));
@@ -353,8 +478,8 @@ hipError_t launch_router(const void* x, const void* w, int64_t n, int hidden, in
   T* gp = static_cast<T*>(gate);
   // k = 8 (GraniteMoE's top-8) has a compile-time path; other k use the runtime one
 #define MEP_ROUTER_CASE(NF_)                                                                               \
-  if (k == 8) router_kernel<DT, NF_, 8><<<grid, kWaves * 64, 0, stream>>>(xp, wp, n, hidden, k, idx, gp, logits); \
-  else router_kernel<DT, NF_, 0><<<grid, kWaves * 64, 0, stream>>>(xp, wp, n, hidden, k, idx, gp, logits);
+  if (k == 8) router_kernel<DT, NF_, 8><<<grid, kWaves * 64, 0, stream>>>(xp, wp, n, hidden, k, idx, gp, logits, hist); \
+  else router_kernel<DT, NF_, 0><<<grid, kWaves * 64, 0, stream>>>(xp, wp, n, hidden, k, idx, gp, logits, hist);
   switch (E) {
     case 16: MEP_ROUTER_CASE(1) break;
     case 32: MEP_ROUTER_CASE(2) break;
@@ -366,6 +491,16 @@ hipError_t launch_router(const void* x, const void* w, int64_t n, int hidden, in
 }
 
 }  // namespace
+
+hipError_t launch_router_with_hist(const void* x, const void* w, int64_t n, int hidden, int E, int k, int dtype,
+                                   int64_t* idx, void* gate, float* logits, int32_t* bc, uint32_t* header,
+                                   uint32_t* flags, int32_t* tables, const uint8_t* valid, int n_blocks,
+                                   hipStream_t stream) {
+  RouterHist h{bc, header, flags, tables, valid, n_blocks};
+  return dtype == MEP_DTYPE_BF16 ? launch_router<MEP_DTYPE_BF16>(x, w, n, hidden, E, k, idx, gate, logits, h, stream)
+                                 : launch_router<MEP_DTYPE_F32>(x, w, n, hidden, E, k, idx, gate, logits, h, stream);
+}
+
 }  // namespace mep
 
 using namespace mep;
@@ -387,11 +522,12 @@ extern "C" int mep_router_topk(const void* x, const void* w_router, int64_t n_to
   MEP_REQUIRE(x && w_router && topk_idx && topk_gate, MEP_ERR_INVALID_ARG,
               "mep_router_topk: null pointer");
   hipStream_t s = static_cast<hipStream_t>(stream);
+  RouterHist none{};
   hipError_t e = dtype == MEP_DTYPE_BF16
                      ? launch_router<MEP_DTYPE_BF16>(x, w_router, n_tokens, hidden, n_experts, top_k,
-                                                     topk_idx, topk_gate, logits, s)
+                                                     topk_idx, topk_gate, logits, none, s)
                      : launch_router<MEP_DTYPE_F32>(x, w_router, n_tokens, hidden, n_experts, top_k,
-                                                    topk_idx, topk_gate, logits, s);
+                                                    topk_idx, topk_gate, logits, none, s);
   MEP_REQUIRE(e == hipSuccess, MEP_ERR_HIP, "mep_router_topk: launch failed: %s", hipGetErrorString(e));
   return MEP_OK;
 }

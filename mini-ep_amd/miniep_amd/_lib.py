@@ -64,6 +64,10 @@ _SIGNATURES = {
                                     _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                     _c_void_p, _c_void_p, _size, _c_void_p]),
     "mep_dispatch_check": (ctypes.c_int, [_c_void_p, _c_void_p]),
+    "mep_route_dispatch_workspace_size": (_size, [_i64, _i32]),
+    "mep_route_dispatch": (ctypes.c_int, [_c_void_p, _c_void_p, _c_void_p, _i64, _i32, _i32, _i32, _i32,
+                                          _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                          _c_void_p, _c_void_p, _c_void_p, _size, _c_void_p]),
     "mep_dispatch_noalloc": (ctypes.c_int, [_c_void_p, _c_void_p, _i64, _i32, _i32,
                                             _c_void_p, _c_void_p, _i32, _i32, _c_void_p,
                                             ctypes.POINTER(_i64), _i32, _i32, _c_void_p, _i32,

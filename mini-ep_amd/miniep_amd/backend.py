@@ -62,6 +62,17 @@ class HipMoEBackend:
         y = ops.grouped_swiglu(x_flat.to(self.w_in.dtype), disp, self.w_in, self.w_out)
         return ops.combine(y, topk_gate, disp.row_of_entry, valid_mask)
 
+    def route_and_call(self, x_flat, w_router, k, valid_mask=None):
+        """The router hook and this backend in one go (Block.forward,
+        modeling.py:193-196): the router kernel also builds the dispatch
+        histograms (ops.route_dispatch), one launch fewer than route() +
+        __call__, same results.  Returns (out, topk_idx, topk_gate)."""
+        x = x_flat.to(self.w_in.dtype)
+        idx, gate, disp = ops.route_dispatch(x, w_router, k, valid_mask, check=self.check)
+        self.last_dispatch = disp
+        y = ops.grouped_swiglu(x, disp, self.w_in, self.w_out)
+        return ops.combine(y, gate, disp.row_of_entry, valid_mask), idx, gate
+
 
 class EPStats:
     """Per-rank counters (ep.py:164-183), kept on the device so that updating

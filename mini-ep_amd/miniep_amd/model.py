@@ -162,15 +162,20 @@ Router = Callable[[torch.Tensor, torch.Tensor, int], tuple[torch.Tensor, torch.T
 class GraniteMoeModel:
     """weights: checkpoint-keyed dict; router: (x_flat, w_router, k) -> (topk_idx,
     topk_gate); moe_backends: one callable per layer with the LocalMoEBackend
-    protocol (x_flat, topk_idx, topk_gate, valid_mask) -> (N, H)."""
+    protocol (x_flat, topk_idx, topk_gate, valid_mask) -> (N, H).  With
+    ``fuse_router``, a backend that has ``route_and_call`` runs the router
+    itself (the fused router + dispatch of HipMoEBackend)."""
 
-    def __init__(self, cfg: ModelConfig, weights: dict, router: Router, moe_backends: Sequence):
+    def __init__(self, cfg: ModelConfig, weights: dict, router: Router, moe_backends: Sequence,
+                 fuse_router: bool = False):
         if len(moe_backends) != cfg.num_hidden_layers:
             raise ValueError(f"{len(moe_backends)} MoE backends for {cfg.num_hidden_layers} layers")
         self.cfg = cfg
         self.w = weights
         self.router = router
         self.moe = list(moe_backends)
+        # backends with route_and_call run the router hook themselves (same results)
+        self.fuse_router = fuse_router
         self.embed = weights["model.embed_tokens.weight"]
         self.rope = RotaryTable(cfg, self.embed.device)
         self._head: torch.Tensor | None = None
@@ -207,8 +212,12 @@ class GraniteMoeModel:
         x = rms_norm(h, self.w[k_["post_ln"]], cfg.rms_norm_eps)
         B, T, H = x.shape
         x_flat = x.reshape(B * T, H)
-        topk_idx, topk_gate = self.router(x_flat, self.w[k_["router"]], cfg.num_experts_per_tok)
-        moe_out = self.moe[layer](x_flat, topk_idx, topk_gate, valid_mask=moe_valid)
+        fused = getattr(self.moe[layer], "route_and_call", None) if self.fuse_router else None
+        if fused is not None:
+            moe_out, _, _ = fused(x_flat, self.w[k_["router"]], cfg.num_experts_per_tok, moe_valid)
+        else:
+            topk_idx, topk_gate = self.router(x_flat, self.w[k_["router"]], cfg.num_experts_per_tok)
+            moe_out = self.moe[layer](x_flat, topk_idx, topk_gate, valid_mask=moe_valid)
         return h + moe_out.view(B, T, H) * cfg.residual_multiplier
 
     @torch.no_grad()
@@ -268,14 +277,15 @@ def greedy_generate(model: GraniteMoeModel, prompts: torch.Tensor, new_tokens: i
 
 def build_hip_model(cfg: ModelConfig, weights: dict, check: bool = False) -> GraniteMoeModel:
     """The model with every MoE block on the HIP path: ``route`` (fused router
-    kernel, fp32 logits) and one ``HipMoEBackend`` per layer."""
+    kernel, fp32 logits) and one ``HipMoEBackend`` per layer, each block's
+    router and dispatch run as one fused call (``route_and_call``)."""
     from .backend import HipMoEBackend, route
 
     backends = []
     for layer in range(cfg.num_hidden_layers):
         k = layer_keys(layer)
         backends.append(HipMoEBackend(weights[k["w_in"]], weights[k["w_out"]], check=check))
-    return GraniteMoeModel(cfg, weights, route, backends)
+    return GraniteMoeModel(cfg, weights, route, backends, fuse_router=True)
 
 
 __all__ = ["ModelConfig", "layer_keys", "random_weights", "rms_norm", "RotaryTable", "KVCache",

@@ -180,6 +180,51 @@ def dispatch(topk_idx: torch.Tensor, valid_mask: torch.Tensor | None, n_experts:
     return Dispatch(counts[:n_local], offsets, perm, row_of_entry, dest, n, k, n_local)
 
 
+def route_dispatch(x_flat: torch.Tensor, w_router: torch.Tensor, k: int, valid_mask: torch.Tensor | None = None,
+                   route_counts: torch.Tensor | None = None, check: bool = True, return_logits: bool = False):
+    """Router + all-local dispatch in one call (mep_route_dispatch, top_k = 8):
+    (topk_idx, topk_gate, Dispatch[, logits]) equal to router_topk followed by
+    dispatch with world-1 tables, one launch fewer.  For other k it makes
+    those two calls."""
+    dev = _require_device(x_flat, w_router, valid_mask, route_counts)
+    x = x_flat.contiguous()
+    w = w_router.to(x.dtype).contiguous()
+    n, h = x.shape
+    e = w.shape[0]
+    if k != 8:
+        out = router_topk(x, w, k, return_logits=return_logits)
+        table = torch.zeros(e, 1, dtype=torch.int32, device=dev)
+        n_rep = torch.ones(e, dtype=torch.int32, device=dev)
+        g2l = torch.arange(e, dtype=torch.int32, device=dev)
+        d = dispatch(out[0], valid_mask, e, table, n_rep, False, None, 0, g2l, e, route_counts=route_counts,
+                     check=check)
+        return (out[0], out[1], d) + ((out[2],) if return_logits else ())
+    if w.shape[1] != h:
+        raise ValueError(f"router weight {tuple(w.shape)} does not match hidden {h}")
+    if route_counts is not None and (route_counts.dtype != torch.int64 or route_counts.numel() != e):
+        raise TypeError("route_counts must be an int64 tensor of n_experts")
+    vm = _mask_u8(valid_mask, n)
+    L = _lib.lib()
+    idx = torch.empty((n, k), dtype=torch.int64, device=dev)
+    gate = torch.empty((n, k), dtype=x.dtype, device=dev)
+    logits = torch.empty((n, e), dtype=torch.float32, device=dev) if return_logits else None
+    ws = torch.empty(max(L.mep_route_dispatch_workspace_size(n, e), 256), dtype=torch.uint8, device=dev)
+    nk = max(n * k, 1)
+    counts = torch.empty(e, dtype=torch.int32, device=dev)
+    offsets = torch.empty(e + 1, dtype=torch.int32, device=dev)
+    perm = torch.empty(nk, dtype=torch.int32, device=dev)
+    row_of_entry = torch.empty(nk, dtype=torch.int32, device=dev)
+    st = _stream(dev)
+    rc = L.mep_route_dispatch(x.data_ptr(), w.data_ptr(), _ptr(vm), n, h, e, k, _dtype_code(x), idx.data_ptr(),
+                              gate.data_ptr(), _ptr(logits), counts.data_ptr(), offsets.data_ptr(), perm.data_ptr(),
+                              row_of_entry.data_ptr(), _ptr(route_counts), ws.data_ptr(), ws.numel(), st)
+    _lib.check(rc, "mep_route_dispatch")
+    if check:
+        _lib.check(L.mep_dispatch_check(ws.data_ptr(), st), "mep_route_dispatch")
+    d = Dispatch(counts, offsets, perm, row_of_entry, None, n, k, e)
+    return (idx, gate, d) + ((logits,) if return_logits else ())
+
+
 # ----------------------------------------------------------------------------
 # grouped SwiGLU experts (modeling.py:83-104) and combine (modeling.py:120-128,144)
 # ----------------------------------------------------------------------------

@@ -118,3 +118,51 @@ def test_router_fused_runtime_k(k):
     ridx, rgate = O.topk_softmax(to_np(logits), k, gate_bf16=True)
     assert np.array_equal(to_np(idx), ridx)
     assert np.abs(to_np(gate) - rgate).max() <= 2 ** -8
+
+
+@pytest.mark.parametrize("e", [16, 32, 64])
+def test_router_fused_tied_logits(e):
+    """Exactly tied logits inside the router kernel (duplicated router rows,
+    all-zero tokens): lower expert id first, as the oracle's rule says."""
+    banner(f"router tied logits e={e}")
+    g = torch.Generator().manual_seed(70 + e)
+    x = torch.randn(640, 1024, generator=g).to(torch.bfloat16)
+    x[::7] = 0                                           # every logit 0: experts 0..7
+    w = (torch.randn(e, 1024, generator=g) * 0.02).to(torch.bfloat16)
+    w[e // 2] = w[3]                                     # tied pairs and a triple in every row
+    w[e - 1] = w[1]
+    w[e - 2] = w[1]
+    idx, gate, logits = ops.router_topk(x.to(DEV), w.to(DEV), 8, return_logits=True)
+    lg = to_np(logits)
+    assert (lg[:, e // 2] == lg[:, 3]).all() and (lg[:, e - 1] == lg[:, 1]).all()
+    ridx, rgate = O.topk_softmax(lg, 8, gate_bf16=True)
+    assert np.array_equal(to_np(idx), ridx)
+    assert to_np(idx)[0].tolist() == list(range(8))
+    assert np.abs(to_np(gate) - rgate).max() <= 2 ** -8
+
+
+@pytest.mark.parametrize("n,e,dtype,masked", [(16384, 32, torch.bfloat16, False), (700, 32, torch.bfloat16, True),
+                                              (63, 16, torch.float32, True), (1, 64, torch.bfloat16, False),
+                                              (40000, 32, torch.bfloat16, True),   # > 512 blocks: scanned
+                                              (0, 32, torch.bfloat16, False)])
+def test_route_dispatch_equals_two_calls(n, e, dtype, masked):
+    """mep_route_dispatch (router kernel with histogram output + scatter) gives
+    the bits of mep_router_topk followed by mep_dispatch."""
+    banner(f"route_dispatch n={n} e={e} {dtype} masked={masked}")
+    L = workloads.make_layer(max(n, 1), seed=n + e, zipf_s=1.2 if e == 32 else 0.0, n_experts=e)
+    x = L.x[:n].to(dtype).to(DEV)
+    w = L.w_router.to(dtype).to(DEV)
+    valid = (torch.rand(n, generator=torch.Generator().manual_seed(3)) < 0.8).to(DEV) if masked else None
+    rc1 = torch.zeros(e, dtype=torch.int64, device=DEV)
+    rc2 = torch.zeros(e, dtype=torch.int64, device=DEV)
+    idx, gate, d = ops.route_dispatch(x, w, 8, valid, route_counts=rc1)
+    idx2, gate2 = ops.router_topk(x, w, 8)
+    table = torch.zeros(e, 1, dtype=torch.int32, device=DEV)
+    n_rep = torch.ones(e, dtype=torch.int32, device=DEV)
+    g2l = torch.arange(e, dtype=torch.int32, device=DEV)
+    d2 = ops.dispatch(idx2, valid, e, table, n_rep, False, None, 0, g2l, e, route_counts=rc2)
+    M = int(d2.offsets[-1])
+    assert torch.equal(idx, idx2) and torch.equal(gate, gate2)
+    assert torch.equal(d.counts, d2.counts) and torch.equal(d.offsets, d2.offsets)
+    assert torch.equal(d.perm[:M], d2.perm[:M]) and torch.equal(d.row_of_entry[: n * 8], d2.row_of_entry[: n * 8])
+    assert torch.equal(rc1, rc2)
