@@ -42,6 +42,10 @@ c4_rank_share (50 timed calls per rank, at least `steps`), the per-stage
 pass, `warmup` steps, the `steps` timed steps, cpu_baseline.  From a light
 load the card's power management first boosts, then throttles the clocks for
 10-15 ms before it settles; the per-stage pass absorbs that transient.
+After the timed steps: ``c2_decode`` (the 32-token decode-shaped layer,
+HBM-bound on expert weights, with its roofline) and ``blas_reference`` (the
+vendor library, hipBLASLt via torch.matmul, on the same GEMM shapes dense, as
+context for the GEMM figures).
 ``cpu_baseline`` times the reference's algorithm restated in PyTorch-CPU
 (fp32) on the same workload on the host's CPU share (and on one core), with
 the numpy oracle's figure beside it.
@@ -151,6 +155,106 @@ def mfma_busy_from_profile() -> dict | None:
             return {"gemm1_pct": float(m.group(1)), "gemm2_pct": float(m.group(2)), "both_pct": float(m.group(3)),
                     "source": f"profiles/{f.name}"}
     return None
+
+
+def decode_detail(dev, calls: int = 200) -> dict:
+    """The decode-shaped layer (32 tokens, bf16, unbiased router: near-uniform
+    load, most experts with 0-16 entries), HBM-bound on streaming the expert
+    weights of the experts it touches.  One call = route + dispatch, GEMM-1,
+    GEMM-2, combine (HipMoEBackend.route_and_call, 5 launches).  At this size
+    the host's enqueue time exceeds the GPU time, so the call is also
+    captured in a HIP graph and replayed (a decode loop would replay it the
+    same way); every replay is checked against the eager output.  HIP events
+    around `calls` back-to-back calls, eager and replayed.  Roofline: the
+    touched experts' weight bytes (3 H I bf16 each) + x, y and outputs per
+    call over the faster call time, vs the 8 TB/s HBM peak."""
+    import torch
+
+    from miniep_amd import HipMoEBackend, workloads
+
+    T, K = 32, workloads.TOP_K
+    lay = workloads.make_layer(T, seed=1)
+    bf = torch.bfloat16
+    x = lay.x.to(bf).to(dev)
+    w_r = lay.w_router.to(bf).to(dev)
+    be = HipMoEBackend(lay.w_in.to(bf).to(dev), lay.w_out.to(bf).to(dev), check=False)
+
+    def timed(fn) -> float:
+        for _ in range(50):
+            fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(calls):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / calls
+
+    eager_ms = timed(lambda: be.route_and_call(x, w_r, K))
+    ref = be.route_and_call(x, w_r, K)[0].clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            be.route_and_call(x, w_r, K)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = be.route_and_call(x, w_r, K)[0]
+    replays_equal = True
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        replays_equal &= bool(torch.equal(out, ref))
+        be.route_and_call(x, w_r, K)
+        torch.cuda.synchronize()
+    ms = timed(graph.replay)
+    torch.cuda.synchronize()
+    replays_equal &= bool(torch.equal(out, ref))
+    touched = int((be.last_dispatch.counts > 0).sum())
+    H, I = workloads.HIDDEN, workloads.INTER
+    nbytes = touched * 3 * H * I * 2 + T * H * 2 * 2 + T * K * H * 2 * 2
+    best = min(ms, eager_ms)
+    return {"workload": "decode-shaped layer, 32 tokens, bf16, unbiased router", "experts_touched": touched,
+            "us_per_call": 1e3 * best, "us_per_call_eager": 1e3 * eager_ms, "us_per_call_graph": 1e3 * ms,
+            "replays_equal_eager": replays_equal, "bytes": nbytes, "GB/s": nbytes / (best / 1e3) / 1e9,
+            "frac_hbm": nbytes / (best / 1e3) / PEAK_HBM_BYTES, "floor_us": 1e6 * nbytes / PEAK_HBM_BYTES,
+            "measures": f"route_and_call (5 launches), {calls} calls back to back, HIP events, launched from Python "
+                        "(eager) and replayed from a HIP graph (graph); us_per_call is the faster of the two"}
+
+
+def blas_reference(dev, M: int) -> dict:
+    """Context for the GEMM figures: the vendor library (hipBLASLt through
+    torch.matmul) on the same GEMM shapes, dense -- all M rows in one matrix,
+    no gather, no scatter, no expert groups -- bf16 in, bf16 out, weights
+    transposed as the checkpoint stores them.  50 warm-up, 50 timed calls."""
+    import torch
+
+    H, I = 1024, 512
+    g = torch.Generator(device=dev).manual_seed(5)
+    a1 = torch.randn(M, H, generator=g, device=dev).to(torch.bfloat16)
+    w1 = torch.randn(2 * I, H, generator=g, device=dev).to(torch.bfloat16)
+    a2 = torch.randn(M, I, generator=g, device=dev).to(torch.bfloat16)
+    w2 = torch.randn(H, I, generator=g, device=dev).to(torch.bfloat16)
+    o = torch.empty(M, H, device=dev, dtype=torch.bfloat16)
+    res = {}
+    for name, fn, flops in (("gemm1_shape", lambda: torch.matmul(a1, w1.t(), out=o), 2.0 * M * H * 2 * I),
+                            ("gemm2_shape", lambda: torch.matmul(a2, w2.t(), out=o), 2.0 * M * I * H)):
+        for _ in range(50):
+            fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(50):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / 50
+        res[name] = {"ms": ms, "TFLOP/s": flops / (ms / 1e3) / 1e12, "frac_mfma": flops / (ms / 1e3) / PEAK_BF16_FLOPS}
+    res["what"] = (f"torch.matmul (hipBLASLt) on dense ({M} x {H}) @ ({H} x {2 * I}) and ({M} x {I}) @ ({I} x {H}), "
+                   "bf16, back to back; the grouped kernels also gather, scatter and split by expert")
+    return res
 
 
 def rank_share_detail(dev, steps: int) -> dict:
@@ -395,6 +499,8 @@ def main(argv=None) -> int:
         "c4_rank_share": c4,
         "rebalance": rebalance,
     }
+    res["c2_decode"] = decode_detail(dev)
+    res["blas_reference"] = blas_reference(dev, M)
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(layer, args.cpu_single_thread_tokens)
     print(json.dumps(res), flush=True)
