@@ -162,8 +162,8 @@ def decode_detail(dev, calls: int = 200) -> dict:
     load, most experts with 0-16 entries), HBM-bound on streaming the expert
     weights of the experts it touches.  One call = route + dispatch, GEMM-1,
     GEMM-2, combine (HipMoEBackend.route_and_call, 5 launches).  At this size
-    the host's enqueue time exceeds the GPU time, so the call is also
-    captured in a HIP graph and replayed (a decode loop would replay it the
+    the host's enqueue time is close to the GPU time, so the call is also
+    captured in a HIP graph and replayed (a decode loop could replay it the
     same way); every replay is checked against the eager output.  HIP events
     around `calls` back-to-back calls, eager and replayed.  Roofline: the
     touched experts' weight bytes (3 H I bf16 each) + x, y and outputs per
