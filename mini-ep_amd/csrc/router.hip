@@ -298,6 +298,62 @@ __device__ void select_topk_wave(const float* lg, int ld, int64_t t0, int64_t n_
   }
 }
 
+// The end of every router kernel: the wave's 16 x E logit tile (MFMA C
+// layout: lane holds rows 4*(lane/16) + i, column lane%16 of each 16-column
+// fragment) goes to the wave's LDS rows, optionally to `logits`, then the
+// selection, the gates and (fused path) the workgroup's dispatch histogram.
+// Called by every thread of the workgroup (it contains barriers).
+template <int DT, int E, int KC>
+__device__ __forceinline__ void router_tail(const f32x4* acc, float (*lgw)[E + 1], uint64_t* keysw, float* sel_valw,
+                                            int* sel_idxw, float* rsumw, int* s_cnt, int64_t t0, int64_t n_tokens,
+                                            int k, int64_t* __restrict__ topk_idx,
+                                            typename Elem<DT>::T* __restrict__ gate, float* __restrict__ logits,
+                                            const RouterHist& hist) {
+  constexpr int NF = E / 16;
+  const int tid = threadIdx.x, lane = lane_id();
+  const int r = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int nf = 0; nf < NF; ++nf)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) lgw[4 * g + i][nf * 16 + r] = acc[nf][i];
+  constexpr bool kWaveSelect = KC > 0 && KC % 4 == 0 && E % 4 == 0;
+  if constexpr (kWaveSelect) {
+    // the tile is this wave's own: order the LDS writes before the reads
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_wave_barrier();
+  } else {
+    __syncthreads();
+  }
+  if (logits != nullptr) {
+    for (int p = lane; p < kRowsPerWave * E; p += 64) {
+      const int t = p / E;
+      if (t0 + t < n_tokens) logits[(t0 + t) * E + (p - t * E)] = lgw[t][p - t * E];
+    }
+  }
+  if constexpr (kWaveSelect) {
+    select_topk_wave<DT, E, KC>(&lgw[0][0], E + 1, t0, n_tokens, sel_valw, sel_idxw, topk_idx, gate, keysw, E + 2,
+                                hist, s_cnt);
+    if (hist.bc != nullptr) {
+      // the workgroup's histogram is the dispatch's histogram of block b
+      __syncthreads();
+      const int b = blockIdx.x;
+      if (tid < E) hist.bc[static_cast<int64_t>(b) * E + tid] = s_cnt[tid];
+      if (tid == 0) hist.flags[b] = 0u;
+      if (b == 0) {
+        if (tid == 0) hist.header[0] = static_cast<uint32_t>(hist.n_blocks);
+        if (tid < E) {
+          hist.tables[tid] = 0;                    // table[e, 0]: every expert on rank 0
+          hist.tables[E + tid] = 1;                // n_rep[e]
+          hist.tables[2 * E + tid] = tid;          // g2l: identity
+        }
+      }
+    }
+  } else {
+    select_topk_from_lds<DT, E, KC>(&lgw[0][0], E + 1, kRowsPerWave, E, k, t0, n_tokens, sel_valw, sel_idxw, rsumw,
+                                    topk_idx, gate, keysw, E + 2);
+  }
+}
+
 // Logit tiles on the matrix cores.  A workgroup of kWaves waves owns
 // kWaves x 16 tokens; W_r is staged through LDS in K segments of at most
 // kSegBytes (all waves share it), x is streamed straight from HBM into the
@@ -347,101 +403,147 @@ __global__ __launch_bounds__(kWaves * 64) void router_kernel(const typename Elem
 #pragma unroll
   for (int nf = 0; nf < NF; ++nf) acc[nf] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  constexpr int kCpr = kSegElems / kElemsPerChunk;                     // chunks per W row
+  constexpr int kPerThread = E * kCpr / (kWaves * 64);
+  static_assert((E * kCpr) % (kWaves * 64) == 0, "W segment splits evenly");
+  // MFMAs of K block b: the block's weight fragments are all read from LDS
+  // first (independent reads in flight together), then the MFMAs run on them
+  auto block_mfmas = [&](const u32x4 (&xb)[8], int b) {
+    u32x4 wb[8][NF];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int nf = 0; nf < NF; ++nf)
+        wb[j][nf] = *reinterpret_cast<const u32x4*>(
+            ws + (nf * 16 + r) * kRowStride + (b * kBlockElems + (4 * j + g) * kElemsPerChunk) * EB);
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int nf = 0; nf < NF; ++nf) {
+        if constexpr (DT == MEP_DTYPE_BF16) {
+          acc[nf] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              __builtin_bit_cast(bf16x8, xb[j]), __builtin_bit_cast(bf16x8, wb[j][nf]), acc[nf], 0, 0, 0);
+        } else {
+          const float* xf = reinterpret_cast<const float*>(&xb[j]);
+          const float* wf = reinterpret_cast<const float*>(&wb[j][nf]);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) acc[nf] = __builtin_amdgcn_mfma_f32_16x16x4f32(xf[q], wf[q], acc[nf], 0, 0, 0);
+        }
+      }
+  };
   for (int seg = 0; seg < hidden; seg += kSegElems) {
     const int nblk = (hidden - seg) / kBlockElems < kSegBlocks ? (hidden - seg) / kBlockElems : kSegBlocks;
-    // this wave's x for the segment, all loads in flight at once
-    u32x4 xa[kSegBlocks][8];
-#pragma unroll
-    for (int b = 0; b < kSegBlocks; ++b)
-      if (b < nblk)
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-          xa[b][j] = *reinterpret_cast<const u32x4*>(xrow + seg + b * kBlockElems + j * 4 * kElemsPerChunk);
-    // W_r[:, seg : seg + nblk*kBlockElems] -> LDS: every load of the segment is
-    // issued before the first LDS store (16-byte chunks, whole workgroup)
-    constexpr int kCpr = kSegElems / kElemsPerChunk;                   // chunks per W row
-    constexpr int kPerThread = E * kCpr / (kWaves * 64);
-    static_assert((E * kCpr) % (kWaves * 64) == 0, "W segment splits evenly");
+    const bool full = nblk == kSegBlocks;          // every block of the segment is real (H = 1024: always)
+    // W_r[:, seg : seg + nblk*kBlockElems] first, then this wave's x rows: the
+    // weight loads are waited for (LDS staging) before the x loads that follow
+    // them, and the x blocks are then waited for one at a time
     const int live_cpr = nblk * kBlockElems / kElemsPerChunk;
     u32x4 wt[kPerThread];
 #pragma unroll
     for (int i = 0; i < kPerThread; ++i) {
       const int c = tid + i * kWaves * 64, e = c / kCpr, q = c % kCpr;
-      if (q < live_cpr)
+      if (full || q < live_cpr)
         wt[i] = *reinterpret_cast<const u32x4*>(w + static_cast<int64_t>(e) * hidden + seg + q * kElemsPerChunk);
     }
+    asm volatile("" ::: "memory");                 // keep the weight loads ahead of the x loads
+    u32x4 xa[kSegBlocks][8];
+#pragma unroll
+    for (int b = 0; b < kSegBlocks; ++b)
+      if (full || b < nblk)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          xa[b][j] = *reinterpret_cast<const u32x4*>(xrow + seg + b * kBlockElems + j * 4 * kElemsPerChunk);
     __syncthreads();                               // previous segment's readers are done
 #pragma unroll
     for (int i = 0; i < kPerThread; ++i) {
       const int c = tid + i * kWaves * 64, e = c / kCpr, q = c % kCpr;
-      if (q < live_cpr) *reinterpret_cast<u32x4*>(ws + e * kRowStride + q * 16) = wt[i];
+      if (full || q < live_cpr) *reinterpret_cast<u32x4*>(ws + e * kRowStride + q * 16) = wt[i];
     }
     __syncthreads();
 #pragma unroll
     for (int b = 0; b < kSegBlocks; ++b) {
-      if (b >= nblk) break;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-#pragma unroll
-        for (int nf = 0; nf < NF; ++nf) {
-          const u32x4 wb = *reinterpret_cast<const u32x4*>(
-              ws + (nf * 16 + r) * kRowStride + (b * kBlockElems + (4 * j + g) * kElemsPerChunk) * EB);
-          if constexpr (DT == MEP_DTYPE_BF16) {
-            acc[nf] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                __builtin_bit_cast(bf16x8, xa[b][j]), __builtin_bit_cast(bf16x8, wb), acc[nf], 0, 0, 0);
-          } else {
-            const float* xf = reinterpret_cast<const float*>(&xa[b][j]);
-            const float* wf = reinterpret_cast<const float*>(&wb);
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-              acc[nf] = __builtin_amdgcn_mfma_f32_16x16x4f32(xf[q], wf[q], acc[nf], 0, 0, 0);
-          }
-        }
-      }
+      if (!full && b >= nblk) break;
+      block_mfmas(xa[b], b);
     }
   }
-  // C layout of the 16x16 MFMA: lane holds rows 4*(lane/16) + i, column lane%16.
-#pragma unroll
-  for (int nf = 0; nf < NF; ++nf)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) lg[wave][4 * g + i][nf * 16 + r] = acc[nf][i];
-  constexpr bool kWaveSelect = KC > 0 && KC % 4 == 0 && E % 4 == 0;
-  if constexpr (kWaveSelect) {
-    // the tile is this wave's own: order the LDS writes before the reads
-    __builtin_amdgcn_s_waitcnt(0xC07F);
-    __builtin_amdgcn_wave_barrier();
-  } else {
-    __syncthreads();
-  }
+  router_tail<DT, E, KC>(acc, lg[wave], keys[wave], sel_val[wave], sel_idx[wave], rsum[wave], s_cnt, t0, n_tokens, k,
+                         topk_idx, gate, logits, hist);
+}
 
-  if (logits != nullptr) {
-    for (int p = lane; p < kRowsPerWave * E; p += 64) {
-      const int t = p / E;
-      if (t0 + t < n_tokens) logits[(t0 + t) * E + (p - t * E)] = lg[wave][t][p - t * E];
+// The router of the GraniteMoE shape: bf16, 32 experts, top-8, hidden a
+// multiple of 1024 (NSEG segments of 1024), everything else as router_kernel.
+// With the hidden size a compile-time constant every address is a base plus
+// an immediate, so per K segment the workgroup issues its W_r loads first
+// (16 x 16 B per thread), then each wave its 16 x rows (32 x 16 B per lane,
+// all in flight), stages W_r in LDS as soon as its loads have landed, and
+// runs the MFMAs of each 256-wide K block as that block of x arrives, with
+// the block's 16 weight fragments read from LDS before its 16 MFMAs (read
+// and multiply interleaved one by one, the LDS latency is paid 64 times).
+template <int NSEG>
+__global__ __launch_bounds__(kWaves * 64) void router32_kernel(const uint16_t* __restrict__ x,
+                                                               const uint16_t* __restrict__ w, int64_t n_tokens,
+                                                               int64_t* __restrict__ topk_idx,
+                                                               uint16_t* __restrict__ gate,
+                                                               float* __restrict__ logits, RouterHist hist) {
+  constexpr int E = 32, NF = 2, KC = 8, H = 1024 * NSEG;
+  constexpr int kRowStride = 1024 * 2 + 16;        // bytes of one W_r row segment in LDS (16 B pad: conflict-free)
+  __shared__ __attribute__((aligned(16))) unsigned char ws[E * kRowStride];
+  __shared__ float lg[kWaves][kRowsPerWave][E + 1];
+  __shared__ __attribute__((aligned(16))) uint64_t keys[kWaves][kRowsPerWave * (E + 2)];
+  __shared__ __attribute__((aligned(16))) float sel_val[kWaves][kRowsPerWave * KC];
+  __shared__ int sel_idx[kWaves][kRowsPerWave * KC];
+  __shared__ float rsum[kWaves][kRowsPerWave];
+  __shared__ int s_cnt[E];
+
+  const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  if (tid < E) s_cnt[tid] = 0;                    // published by the first barrier below
+  const int64_t t0 = (static_cast<int64_t>(blockIdx.x) * kWaves + wave) * kRowsPerWave;
+  int64_t tok = t0 + r;
+  if (tok >= n_tokens) tok = n_tokens - 1;        // in-bounds read, result discarded
+  const uint16_t* xrow = x + tok * H + g * 8;
+  // W_r chunk i of this thread: row (tid >> 7) + 2 i, 16 bytes at column (tid & 127) * 8
+  const uint16_t* wrow = w + static_cast<int64_t>(tid >> 7) * H + (tid & 127) * 8;
+  const int wlds = (tid >> 7) * kRowStride + (tid & 127) * 16;
+
+  f32x4 acc[NF];
+#pragma unroll
+  for (int nf = 0; nf < NF; ++nf) acc[nf] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int seg = 0; seg < NSEG; ++seg) {
+    u32x4 wt[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) wt[i] = *reinterpret_cast<const u32x4*>(wrow + 2 * i * H + seg * 1024);
+    asm volatile("" ::: "memory");               // the weight loads go out first
+    u32x4 xa[4][8];
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) xa[b][j] = *reinterpret_cast<const u32x4*>(xrow + seg * 1024 + b * 256 + j * 32);
+    if (seg > 0) __syncthreads();                 // the previous segment's fragment reads are done
+#pragma unroll
+    for (int i = 0; i < 16; ++i) *reinterpret_cast<u32x4*>(ws + wlds + 2 * i * kRowStride) = wt[i];
+    __syncthreads();
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      u32x4 wb[8][NF];
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int nf = 0; nf < NF; ++nf)
+          wb[j][nf] = *reinterpret_cast<const u32x4*>(ws + (nf * 16 + r) * kRowStride + (b * 256 + (4 * j + g) * 8) * 2);
+      __builtin_amdgcn_sched_barrier(0);          // all 16 fragment reads issued before the MFMAs
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int nf = 0; nf < NF; ++nf)
+          acc[nf] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xa[b][j]),
+                                                            __builtin_bit_cast(bf16x8, wb[j][nf]), acc[nf], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
-  if constexpr (kWaveSelect) {
-    select_topk_wave<DT, E, KC>(&lg[wave][0][0], E + 1, t0, n_tokens, sel_val[wave], sel_idx[wave], topk_idx, gate,
-                                keys[wave], E + 2, hist, s_cnt);
-    if (hist.bc != nullptr) {
-      // the workgroup's histogram is the dispatch's histogram of block b
-      __syncthreads();
-      const int b = blockIdx.x;
-      if (tid < E) hist.bc[static_cast<int64_t>(b) * E + tid] = s_cnt[tid];
-      if (tid == 0) hist.flags[b] = 0u;
-      if (b == 0) {
-        if (tid == 0) hist.header[0] = static_cast<uint32_t>(hist.n_blocks);
-        if (tid < E) {
-          hist.tables[tid] = 0;                    // table[e, 0]: every expert on rank 0
-          hist.tables[E + tid] = 1;                // n_rep[e]
-          hist.tables[2 * E + tid] = tid;          // g2l: identity
-        }
-      }
-    }
-  } else {
-    select_topk_from_lds<DT, E, KC>(&lg[wave][0][0], E + 1, kRowsPerWave, E, k, t0, n_tokens, sel_val[wave],
-                                    sel_idx[wave], rsum[wave], topk_idx, gate, keys[wave], E + 2);
-  }
+  router_tail<MEP_DTYPE_BF16, E, KC>(acc, lg[wave], keys[wave], sel_val[wave], sel_idx[wave], rsum[wave], s_cnt, t0,
+                                      n_tokens, KC, topk_idx, gate, logits, hist);
 }
 
 // Top-k + softmax of precomputed logits: one wave per `rows` tokens.
@@ -476,6 +578,18 @@ hipError_t launch_router(const void* x, const void* w, int64_t n, int hidden, in
   const T* xp = static_cast<const T*>(x);
   const T* wp = static_cast<const T*>(w);
   T* gp = static_cast<T*>(gate);
+  if constexpr (DT == MEP_DTYPE_BF16) {
+    // GraniteMoE's shape: the specialised kernel
+    if (E == 32 && k == 8 && (hidden == 1024 || hidden == 2048 || hidden == 4096)) {
+      const uint16_t* xb = static_cast<const uint16_t*>(x);
+      const uint16_t* wbp = static_cast<const uint16_t*>(w);
+      uint16_t* gb = static_cast<uint16_t*>(gate);
+      if (hidden == 1024) router32_kernel<1><<<grid, kWaves * 64, 0, stream>>>(xb, wbp, n, idx, gb, logits, hist);
+      else if (hidden == 2048) router32_kernel<2><<<grid, kWaves * 64, 0, stream>>>(xb, wbp, n, idx, gb, logits, hist);
+      else router32_kernel<4><<<grid, kWaves * 64, 0, stream>>>(xb, wbp, n, idx, gb, logits, hist);
+      return hipGetLastError();
+    }
+  }
   // k = 8 (GraniteMoE's top-8) has a compile-time path; other k use the runtime one
 #define MEP_ROUTER_CASE(NF_)                                                                               \
   if (k == 8) router_kernel<DT, NF_, 8><<<grid, kWaves * 64, 0, stream>>>(xp, wp, n, hidden, k, idx, gp, logits, hist); \
