@@ -10,28 +10,31 @@ weights N(0, 0.02).  One step = the whole hot path over the batch, inputs
 already resident in HBM:
 
     router (GEMV + top-8 + softmax, with the dispatch's per-block expert
-    histograms) -> dispatch scatter (stable rank, permutation) -> GEMM-1 +
-    SwiGLU (gathered rows) -> GEMM-2 (scattered to (token, slot) cells) ->
-    combine (gate-weighted slot-order sum)
+    histograms) -> dispatch scatter (stable rank, permutation) -> grouped
+    experts, one launch: GEMM-1 + SwiGLU (gathered rows) and GEMM-2
+    (scattered to (token, slot) cells), each XCD's GEMM-2 tiles starting
+    once their rows' GEMM-1 tiles are done -> combine (gate-weighted
+    slot-order sum)
 
 Prints one JSON line.  ``value`` is tokens/s over the timed steps (wall
 clock, synchronised on both sides).  Inside the timed steps, HIP events on the
-launch stream mark GEMM-1's start, the boundary of the two GEMMs and GEMM-2's
-end: ``roofline`` is for GEMM-1, the dominant kernel (2/3 of the flops),
-2*M*H*2I flops per launch over its mean event time, vs the 2.5 PFLOP/s dense
-bf16 MFMA peak, and ``grouped_gemm_mfma_util_pct`` is both GEMMs' algorithmic
-flops over their mean event times (``timed_gemms``) against the same peak.
+launch stream bracket the grouped-experts launch: ``roofline`` is for that
+kernel, the dominant one (both GEMMs: 6*M*H*I flops per launch) over its mean
+event time, vs the 2.5 PFLOP/s dense bf16 MFMA peak, and
+``grouped_gemm_mfma_util_pct`` is the same ratio in percent (``timed_gemms``).
 The per-stage breakdown (``stages``) comes from events around every stage in
-a pass of at least 50 steps before the warm-up: an event record between two
-kernels costs the GPU a few microseconds, so recording all of them inside the
-timed region would understate the throughput of the path.
-``roofline.traffic`` is GEMM-1's HBM bytes per launch from the committed
-counter summary (``profiles/*hbm_traffic.md``: rocprofv3 FETCH_SIZE and
-WRITE_SIZE passes over this script, scaled by what the same counters read for
-the 256 MiB calibration copy this script issues first), or null when that
-summary is absent.  ``mfma_busy_counters`` is the hardware's own view from
-the committed counter summary (``profiles/*mfma_busy*.md``: MFMA busy cycles
-over active cycles).
+a pass of at least 50 steps before the warm-up, with the two GEMMs launched
+separately there (mep_swiglu_gate_up, mep_swiglu_down) so that each has its
+own time: an event record between two kernels costs the GPU a few
+microseconds, so recording all of them inside the timed region would
+understate the throughput of the path.
+``roofline.traffic`` is the grouped-experts kernel's HBM bytes per launch from
+the committed counter summary (``profiles/*hbm_traffic.md``: rocprofv3
+FETCH_SIZE and WRITE_SIZE passes over this script, scaled by what the same
+counters read for the 256 MiB calibration copy this script issues first), or
+null when that summary is absent.  ``mfma_busy_counters`` is the hardware's
+own view from the committed counter summary (``profiles/*mfma_busy*.md``: MFMA
+busy cycles over active cycles).
 ``c4_rank_share`` (outside the timed region):
 one rank's share of 4-way expert parallelism under the reference's balanced
 plan at T=8192, per rank.  ``rebalance`` (before c4_rank_share): the live
@@ -147,13 +150,13 @@ def cpu_baseline(layer, single_tokens: int, reps: int = 3) -> dict:
 
 
 def mfma_busy_from_profile() -> dict | None:
-    """MFMA busy / active cycles of the two GEMMs from the committed counter
-    summary (rocprofv3 SQ_VALU_MFMA_BUSY_CYCLES and GRBM_GUI_ACTIVE), if any."""
+    """MFMA busy / active cycles of the grouped-experts launch from the
+    committed counter summary (rocprofv3 SQ_VALU_MFMA_BUSY_CYCLES and
+    GRBM_GUI_ACTIVE), if any."""
     for f in sorted((ROOT / "profiles").glob("*mfma_busy*.md")):
-        m = re.search(r"mfma_busy_pct = gemm1 ([0-9.]+), gemm2 ([0-9.]+), both ([0-9.]+)", f.read_text())
+        m = re.search(r"mfma_busy_pct = experts ([0-9.]+)", f.read_text())
         if m:
-            return {"gemm1_pct": float(m.group(1)), "gemm2_pct": float(m.group(2)), "both_pct": float(m.group(3)),
-                    "source": f"profiles/{f.name}"}
+            return {"experts_pct": float(m.group(1)), "source": f"profiles/{f.name}"}
     return None
 
 
@@ -263,10 +266,9 @@ def rank_share_detail(dev, steps: int) -> dict:
     fixture tests/golden/plan_balanced.json), layer 2 (8 owned + 2 replica
     experts per rank), T=8192 Zipf(1.1)-routed bf16 tokens from 4 source
     segments (round-robin counters zeroed, as after reset_rr).  Per rank:
-    dispatch in share mode + GEMM-1 + GEMM-2 on its local experts, HIP events
-    around `steps` back-to-back calls (GPU-bound: replaying the call from a
-    captured graph measured no faster).  A share of 12.7-20.1k rows is one to
-    two rounds of 256x256 tiles, so its time hardly depends on its rows."""
+    dispatch in share mode + the grouped experts (one launch) on its local
+    experts, HIP events around `steps` back-to-back calls (GPU-bound:
+    replaying the call from a captured graph measured no faster)."""
     import torch
 
     from miniep_amd import HipEPShareBackend, Placement, ops, workloads
@@ -298,7 +300,7 @@ def rank_share_detail(dev, steps: int) -> dict:
         ranks.append({"rank": r, "local_experts": len(ids), "rows": rows, "ms": ms,
                       "TFLOP/s": 6.0 * rows * H * I / (ms / 1e3) / 1e12})
     return {"workload": "rank share of 4-way EP, plan_balanced layer 2, T=8192 Zipf(1.1), 4 sources, bf16",
-            "measures": "dispatch (share mode) + GEMM-1 + GEMM-2 per call, back to back", "ranks": ranks}
+            "measures": "dispatch (share mode) + grouped experts (one launch) per call, back to back", "ranks": ranks}
 
 
 def rebalance_detail(dev) -> dict:
@@ -333,7 +335,7 @@ def rebalance_detail(dev) -> dict:
 
 
 def traffic_from_profile() -> dict | None:
-    """GEMM-1 HBM bytes per launch from the committed counter summary, if any."""
+    """Grouped-experts HBM bytes per launch from the committed counter summary, if any."""
     for f in sorted((ROOT / "profiles").glob("*hbm_traffic.md")):
         m = re.search(r"traffic_bytes_per_launch\s*=\s*([0-9.eE+]+)", f.read_text())
         if m:
@@ -369,32 +371,31 @@ def main(argv=None) -> int:
     out = torch.empty(T, H, dtype=bf, device=dev)
     stages = ["route_dispatch", "gemm1_swiglu", "gemm2_scatter", "combine"]
 
-    def step(ev=None, g=None):
-        """One pass of the hot path; `ev` = 5 events around every stage,
-        `g` = 3 events around the two GEMMs only.  The router and the dispatch
-        run as one call (router kernel with the dispatch histograms, then the
-        dispatch's scatter kernel)."""
-        if ev is not None:
-            ev[0].record()
+    def step(g=None):
+        """One pass of the hot path (4 calls: router with the dispatch
+        histograms + dispatch scatter, the grouped experts in one launch,
+        combine); `g` = 2 events around the grouped-experts launch."""
         idx, gate, disp = ops.route_dispatch(x, w_r, K, None, check=False)
-        if ev is not None:
-            ev[1].record()
         if g is not None:
             g[0].record()
-        ops.swiglu_gate_up(x, disp, w_in, act)
+        ops.grouped_swiglu(x, disp, w_in, w_out, y)
         if g is not None:
             g[1].record()
-        if ev is not None:
-            ev[2].record()
-        ops.swiglu_down(act, x, disp, w_out, y)
-        if g is not None:
-            g[2].record()
-        if ev is not None:
-            ev[3].record()
         ops.combine(y, gate, disp.row_of_entry, None, out)
-        if ev is not None:
-            ev[4].record()
         return disp
+
+    def step_split(ev):
+        """The same pass with the two GEMMs launched separately and 5 events
+        around the stages (the per-stage breakdown)."""
+        ev[0].record()
+        idx, gate, disp = ops.route_dispatch(x, w_r, K, None, check=False)
+        ev[1].record()
+        ops.swiglu_gate_up(x, disp, w_in, act)
+        ev[2].record()
+        ops.swiglu_down(act, x, disp, w_out, y)
+        ev[3].record()
+        ops.combine(y, gate, disp.row_of_entry, None, out)
+        ev[4].record()
 
     # calibration copy of known size for the HBM counters (FETCH_SIZE /
     # WRITE_SIZE of this copy scale the kernels' counters to bytes)
@@ -425,7 +426,7 @@ def main(argv=None) -> int:
     n_stage = max(args.steps, 50)
     events = [[torch.cuda.Event(enable_timing=True) for _ in range(len(stages) + 1)] for _ in range(n_stage)]
     for s in range(n_stage):
-        step(events[s])
+        step_split(events[s])
     torch.cuda.synchronize()
     stage_ms = {name: sum(events[s][i].elapsed_time(events[s][i + 1]) for s in range(n_stage)) / n_stage
                 for i, name in enumerate(stages)}
@@ -434,9 +435,9 @@ def main(argv=None) -> int:
         step()
     torch.cuda.synchronize()
 
-    # timed region: wall clock over exactly `steps` steps; events at GEMM-1's
-    # start, between the GEMMs and at GEMM-2's end
-    g_events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    # timed region: wall clock over exactly `steps` steps; events around the
+    # grouped-experts launch
+    g_events = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(args.steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for s in range(args.steps):
@@ -444,8 +445,7 @@ def main(argv=None) -> int:
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_step = wall / args.steps * 1e3
-    g1_ms = sum(e[0].elapsed_time(e[1]) for e in g_events) / args.steps
-    g2_ms = sum(e[1].elapsed_time(e[2]) for e in g_events) / args.steps
+    exp_ms = sum(e[0].elapsed_time(e[1]) for e in g_events) / args.steps
     flops_g1 = 2.0 * M * H * 2 * I
     flops_g2 = 2.0 * M * I * H
     # router: x and W_r in, indices (int64) and gates (bf16) out; dispatch
@@ -465,9 +465,9 @@ def main(argv=None) -> int:
         "combine": {"ms": stage_ms["combine"], "GB/s": combine_bytes / (stage_ms["combine"] / 1e3) / 1e9,
                     "frac_hbm": combine_bytes / (stage_ms["combine"] / 1e3) / PEAK_HBM_BYTES},
     }
-    # north-star figure: both GEMMs of the timed steps, algorithmic flops
-    gemm_util = (flops_g1 + flops_g2) / ((g1_ms + g2_ms) / 1e3) / PEAK_BF16_FLOPS
-    achieved = flops_g1 / (g1_ms / 1e3) / 1e12
+    # north-star figure: both GEMMs of the timed steps (one launch), algorithmic flops
+    gemm_util = (flops_g1 + flops_g2) / (exp_ms / 1e3) / PEAK_BF16_FLOPS
+    achieved = (flops_g1 + flops_g2) / (exp_ms / 1e3) / 1e12
     traffic = traffic_from_profile()
     res = {
         "metric": METRIC,
@@ -486,15 +486,16 @@ def main(argv=None) -> int:
         "config": {"workload": WORKLOAD, "tokens": T, "hidden": H, "experts": E, "top_k": K,
                    "inter": I, "entries": M, "hottest_over_mean": round(hottest, 3)},
         "grouped_gemm_mfma_util_pct": 100.0 * gemm_util,
-        "timed_gemms": {"gemm1_ms": g1_ms, "gemm2_ms": g2_ms, "source": "HIP events inside the timed steps"},
+        "timed_gemms": {"experts_ms": exp_ms, "launches": 1, "source": "HIP events inside the timed steps"},
         "mfma_busy_counters": mfma_busy_from_profile(),
         "layer_tflops": (flops_g1 + flops_g2) / (ms_step / 1e3) / 1e12,
-        "roofline": {"kernel": "moe_gemm_bf16_kernel<true> (GEMM-1: gate/up + SwiGLU)", "bound": "mfma",
+        "roofline": {"kernel": "moe_gemm_bf16_kernel<3> (grouped experts, one launch: GEMM-1 + SwiGLU "
+                               "and GEMM-2 + scatter)", "bound": "mfma",
                      "achieved": achieved, "peak": PEAK_BF16_FLOPS / 1e12, "unit": "TFLOP/s",
                      "frac": achieved * 1e12 / PEAK_BF16_FLOPS,
                      "traffic": traffic["bytes"] if traffic else None,
                      "traffic_source": traffic["source"] if traffic else None,
-                     "flops_per_launch": flops_g1, "mean_launch_ms": g1_ms},
+                     "flops_per_launch": flops_g1 + flops_g2, "mean_launch_ms": exp_ms},
         "stages": detail,
         "c4_rank_share": c4,
         "rebalance": rebalance,

@@ -194,19 +194,34 @@ int mep_route_dispatch(const void* x, const void* w_router, const uint8_t* valid
  *   x (N, H)   w_in (n_local, 2I, H)   w_out (n_local, H, I)   y_entries (N*k, H)
  * max_rows >= offsets[n_local] (e.g. N*k) bounds the launch.
  * Supported: H % 256 == 0, I % 128 == 0.
- * tile_queue: 2 int32 of device memory that are zero before the first call;
- * the bf16 kernels hand out their last round of tiles through them and every
- * launch leaves them zero again.  Launches that may run at the same time (on
- * different streams) need different queues; launches on one stream can share
- * one.  No counterpart in the reference (its experts are a Python loop).
+ * With bf16, I % 256 == 0 and more than 2048 rows, both GEMMs run as ONE
+ * persistent launch: each XCD works through its share of the row tiles, and
+ * a row tile's GEMM-2 tiles start once its GEMM-1 tiles are done.
+ * tile_queue: tile_queue_ints >= mep_experts_queue_ints(max_rows, n_local)
+ * int32 of device memory, zero before the first call; the tiled kernels keep
+ * their schedule there (per-XCD tile counters, per-row-tile GEMM-1
+ * completion counts) and every launch leaves it zero again, except word 10:
+ * sticky error flags that mep_experts_check reports (a GEMM-2 tile that gave
+ * up waiting for its rows after about a second, a queue that no workgroup
+ * drained; either means the results are invalid).  Launches that may run at
+ * the same time (on different streams) need different queues; launches on
+ * one stream can share one.  No counterpart in the reference (its experts
+ * are a Python loop).
  * ---------------------------------------------------------------------- */
+size_t mep_experts_queue_ints(int64_t max_rows, int32_t n_local);
+
+/* Synchronises `stream`, then reads tile_queue's error flags:
+ * MEP_OK, or MEP_ERR_HIP with the reason in mep_last_error(). */
+int mep_experts_check(const int32_t* tile_queue, void* stream);
+
 size_t mep_experts_workspace_size(int64_t max_rows, int32_t inter, int32_t dtype);
 
 int mep_grouped_swiglu(const void* x, int64_t n_tokens, int32_t top_k,
                        const int32_t* perm, const int32_t* offsets, int32_t n_local,
                        int64_t max_rows, const void* w_in, const void* w_out,
                        int32_t hidden, int32_t inter, int32_t dtype, void* y_entries,
-                       void* workspace, size_t workspace_bytes, int32_t* tile_queue, void* stream);
+                       void* workspace, size_t workspace_bytes, int32_t* tile_queue,
+                       size_t tile_queue_ints, void* stream);
 
 /* The two launches of mep_grouped_swiglu as separate calls, for callers that
  * schedule or time them individually (same kernels, same results):
@@ -217,12 +232,13 @@ int mep_grouped_swiglu(const void* x, int64_t n_tokens, int32_t top_k,
 int mep_swiglu_gate_up(const void* x, int64_t n_tokens, int32_t top_k, const int32_t* perm,
                        const int32_t* offsets, int32_t n_local, int64_t max_rows,
                        const void* w_in, int32_t hidden, int32_t inter, int32_t dtype,
-                       void* act, size_t act_bytes, int32_t* tile_queue, void* stream);
+                       void* act, size_t act_bytes, int32_t* tile_queue, size_t tile_queue_ints,
+                       void* stream);
 
 int mep_swiglu_down(const void* act, int64_t n_tokens, int32_t top_k, const int32_t* perm,
                     const int32_t* offsets, int32_t n_local, int64_t max_rows,
                     const void* w_out, int32_t hidden, int32_t inter, int32_t dtype,
-                    void* y_entries, int32_t* tile_queue, void* stream);
+                    void* y_entries, int32_t* tile_queue, size_t tile_queue_ints, void* stream);
 
 /* Expert weight slots (the live re-slice of server.py:51-62 / weights.py:37-61
  * without re-reading a checkpoint for experts that stay):
@@ -243,7 +259,7 @@ int mep_grouped_swiglu_slots(const void* x, int64_t n_tokens, int32_t top_k,
                              int64_t max_rows, const void* w_in, const void* w_out,
                              const int32_t* w_slot, int32_t hidden, int32_t inter, int32_t dtype,
                              void* y_entries, void* workspace, size_t workspace_bytes,
-                             int32_t* tile_queue, void* stream);
+                             int32_t* tile_queue, size_t tile_queue_ints, void* stream);
 
 int mep_copy_experts(const void* src_in, const void* src_out, int32_t n_src,
                      void* dst_in, void* dst_out, int32_t n_slots,

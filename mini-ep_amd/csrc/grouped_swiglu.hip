@@ -78,7 +78,6 @@ struct GemmParams {
   uint32_t a_bytes;          // size of A in bytes (< 4 GiB)
   uint32_t k_magic;          // entry / top_k == umulhi(entry, k_magic) >> k_shift for entry < 2^31
   int k_shift;
-  int* tile_queue;           // bf16 kernels: 2 counters, zero before and after every launch
 };
 
 // Round-up reciprocal for exact division by d of every n < 2^31: with
@@ -473,7 +472,7 @@ constexpr int NLMAX = 256;
 // after the stage buffers; the tables follow it
 constexpr int STG_ROWS = 8, STG_WAVE = STG_ROWS * 256, STG = 4 * HALF;
 constexpr int TABLES = STG + NW * STG_WAVE;
-constexpr int LDS_BYTES = TABLES + (2 * (NLMAX + 1) + 2 * BM + 2 + NLMAX) * 4;
+constexpr int LDS_BYTES = TABLES + (2 * (NLMAX + 1) + 2 * BM + 4 + NLMAX) * 4;
 static_assert(LDS_BYTES <= 160 * 1024, "LDS budget of one workgroup");
 // buffer resource word 3 for raw 32-bit buffer access on gfx9-family parts
 constexpr int kBufWord3 = 0x00020000;
@@ -481,6 +480,43 @@ static_assert(BN * RB == HALF, "A and weight rows of a stage are the same size")
 static_assert((BM + BN) / 8 == NW * BPW, "DMA blocks cover the stage");
 static_assert(BPW == NF, "one DMA block per MFMA group of an odd step");
 }  // namespace bfk
+
+// Words of the bf16 tiled kernels' schedule buffer (`tile_queue` of the C ABI,
+// int32, sched::words(max_rows, n_local) of them):
+//   [0, 8)           items taken from each XCD's queue
+//   8                workgroups finished
+//   9                items computed
+//   10               error flags, sticky (never cleared by a launch):
+//                    kFlagWait  a GEMM-2 tile gave up waiting for its rows
+//                    kFlagDrain items computed != items listed (never expected)
+//   11               bit per drained queue
+//   [16, 16 + RT)    GEMM-1 column tiles finished per row tile (kModeBoth)
+// Every launch leaves every word but 10 zero.
+namespace sched {
+constexpr int kQueue = 0, kDone = 8, kItems = 9, kFlags = 10, kDrained = 11, kRowDone = 16;
+constexpr int kFlagWait = 1, kFlagDrain = 2;
+constexpr int kWaitLimit = 1 << 20;            // polls of one row counter (about a second)
+// row tiles of max_rows rows over n_local experts: each expert adds at most one partial tile
+inline int64_t words(int64_t max_rows, int n_local) { return kRowDone + (max_rows + 255) / 256 + n_local; }
+}  // namespace sched
+
+constexpr int kModeGateUp = 1, kModeDown = 2, kModeBoth = 3;
+struct MoeParams {
+  const void* x;             // (n_tokens, H)
+  void* act;                 // (max_rows, I): GEMM-1's output, GEMM-2's A operand
+  void* y;                   // (N*k, H) y_entries
+  const int32_t* perm;       // row -> flat entry id
+  const int32_t* offsets;    // (n_local + 1) row offsets per local expert
+  const int32_t* w_slot;     // (n_local,) slot of local expert j, or NULL: slot j
+  const void* w_in;          // (slots, 2I, H)
+  const void* w_out;         // (slots, H, I)
+  int n_local, top_k, H, I;
+  uint32_t x_bytes, act_bytes;   // sizes of x and act in bytes (< 4 GiB)
+  uint32_t k_magic;          // entry / top_k == umulhi(entry, k_magic) >> k_shift (k_magic 0: k = 1)
+  int k_shift;
+  int n_queues;              // queues (XCDs), a power of two <= 8
+  int* sched;
+};
 
 // 16x16x32 bf16 MFMA with the accumulator in VGPRs; src0 = weight
 // fragment, src1 = row fragment, so the result is C^T (lane: one row, 4
@@ -516,95 +552,163 @@ __device__ __forceinline__ void buffer_lds_16(const unsigned char* base, int byt
       (__attribute__((address_space(3))) void*)lds, 16, voff, __builtin_amdgcn_readfirstlane(soff), 0, 0);
 }
 
-template <bool GEMM1>
-__global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
+// Hardware id of the XCD this wave runs on (0..7 on an 8-XCD part).
+__device__ __forceinline__ int xcc_id() {
+  unsigned v;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+  return static_cast<int>(v & 15u);
+}
+
+// Grouped GEMM over 256-row tiles of the dispatched rows: GEMM-1 + SwiGLU
+// (MODE kModeGateUp), GEMM-2 + scatter (kModeDown), or both in one launch
+// (kModeBoth).  Tiles are (row tile, column tile) pairs; a row tile is 256
+// consecutive rows of one expert (an expert's last one may be partial).
+//
+// Queues.  The row tiles are split into n_queues contiguous ranges, one per
+// XCD, and the workgroups of an XCD (read from the hardware, not assumed
+// from the workgroup id) take that range's tiles in order, one at a time,
+// through the XCD's counter in `sched`: the tiles of one expert run on one
+// XCD and share its weights in that XCD's L2, and the column tiles of a row
+// tile, taken one after the other, share the row tile's A rows there.  The
+// XCDs do not run at one speed (the same work takes up to 8 % longer on one
+// than on another), so a workgroup whose queue is drained takes the
+// remaining tiles of the other queues (a bit per drained queue in `sched`
+// spares it the atomics on those).
+// In kModeBoth a queue lists GEMM-1's tiles of its row tiles, then GEMM-2's
+// (measured: GEMM-2 row tiles 4 or 8 row tiles behind GEMM-1's, to reuse act
+// from L2, ran 4-15 % slower than this order).  A GEMM-2 tile needs every GEMM-1 column tile of its row tile
+// done (act is its A operand): each GEMM-1 tile, once its stores are
+// complete, adds one to its row tile's counter in `sched`, and a GEMM-2 tile
+// starts when that counter is full.  GEMM-1 stores act with device scope
+// (written through to memory), so a GEMM-2 tile on any XCD reads the final
+// rows: its XCD's caches hold no line of them (it reads them only after they
+// are final, and every launch starts with clean caches).  The wait is checked
+// four steps before the tile in front of it would prefetch the GEMM-2
+// tile's first stages; if it is not met there, the workgroup finishes its tile, counts it, and
+// waits between tiles with nothing of its own pending: a workgroup that waits
+// holds no unfinished tile, and the tiles it waits for come earlier in the
+// queue than the one it waits with, so every wait ends.  A wait that still
+// exceeds sched::kWaitLimit polls sets sched flag kFlagWait and goes on.
+// Which workgroup computes a tile never changes its result, so the bits are
+// those of two separate launches.
+// Device-scope atomics of a single lane (thread 0 of a workgroup).  The
+// offset (and for reads the addend) is an opaque zero: with a uniform
+// address the compiler combines the atomic across the wave and reads its
+// result back into a scalar right away, which stalls the wave on every
+// memory operation it has in flight (the stage DMA included); and it turns
+// an add of a known 0 into an atomic load, which may be answered from a
+// cache line another XCD has since changed.  With the opaque zero these stay
+// one read-modify-write each, performed where every XCD's atomics are.
+__device__ __forceinline__ int opaque_zero() {
+  int z;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+  return z;
+}
+__device__ __forceinline__ int atomic_add_1(int* p, int v) { return atomicAdd(p + opaque_zero(), v); }
+__device__ __forceinline__ int atomic_read(int* p) {
+  const int z = opaque_zero();
+  return atomicAdd(p + z, z);
+}
+__device__ __forceinline__ int atomic_or_1(int* p, int v) { return atomicOr(p + opaque_zero(), v); }
+
+// 16-byte store with device scope (sc1): written through to memory, where a
+// later read from another XCD finds it.  base / bytes as in buffer_lds_16.
+__device__ __forceinline__ void store_dev_16(void* base, uint32_t bytes, uint32_t voff, const u32x4& v) {
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(b >> 32)));
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(b & 0xFFFFFFFFu)));
+  const uint64_t bs = (static_cast<uint64_t>(hi) << 32) | lo;
+  __builtin_amdgcn_raw_buffer_store_b128(
+      v, __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(bs), 0,
+                                           __builtin_amdgcn_readfirstlane(static_cast<int>(bytes)), bfk::kBufWord3),
+      voff, 0, 16 /* sc1: device scope */);
+}
+
+template <int MODE>
+__global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(MoeParams p) {
   using namespace bfk;
+  constexpr bool BOTH = MODE == kModeBoth;
   __shared__ __attribute__((aligned(16))) unsigned char smem[LDS_BYTES];
-  int* const s_prefix = reinterpret_cast<int*>(smem + TABLES);         // [NLMAX + 1] tiles before expert j
+  int* const s_prefix = reinterpret_cast<int*>(smem + TABLES);         // [NLMAX + 1] row tiles before expert j
   int* const s_off = s_prefix + NLMAX + 1;                             // [NLMAX + 1] row offsets
   int* const s_rows = s_off + NLMAX + 1;                               // [2][BM] row maps
-  int* const s_pool = s_rows + 2 * BM;                                 // [2] pool items taken
-  int* const s_slot = s_pool + 2;                                      // [NLMAX] weight slot of expert j
+  int* const s_msg = s_rows + 2 * BM;                                  // [4] answers of thread 0's atomics
+  int* const s_slot = s_msg + 4;                                       // [NLMAX] weight slot of expert j
 
   const int tid = threadIdx.x;
   // wave index as a scalar: keeps per-wave choices (A or weight rows, buffer
   // resources) in SGPRs
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
-  const int K = p.K;
-  const int KD = K / (2 * KS);                // stages per tile (a multiple of 4, >= 4)
-  const int KT = 2 * KD;                      // MFMA steps per tile
   const int nl = p.n_local;
+  const int n1 = p.I / (BN / 2), n2 = p.H / BN;  // column tiles of a row tile: GEMM-1, GEMM-2
+  int* const sched = p.sched;
 
-  // ---- tile table ---------------------------------------------------------------
+  // ---- row tiles ------------------------------------------------------------------
   for (int j = tid; j <= nl; j += NT) s_off[j] = p.offsets[j];
   for (int j = tid; j < nl; j += NT) s_slot[j] = p.w_slot != nullptr ? p.w_slot[j] : j;
   __syncthreads();
-  if (tid < 64) scan_units<BM>(s_off, s_prefix, nl, p.n_tiles_n);
+  if (tid < 64) scan_units<BM>(s_off, s_prefix, nl, 1);
   __syncthreads();
-  const int total = __builtin_amdgcn_readfirstlane(s_prefix[nl]);
-  // Work items.  XCD x owns tiles [lo(x), hi(x)); its nslots workgroups take
-  // items slot, slot + nslots, ... for the n_priv whole rounds.  The tiles
-  // left over after the whole rounds of every XCD form one pool (XCD 0's,
-  // then XCD 1's, ...) that workgroups take one at a time through an atomic
-  // counter once their own rounds are done, so the last round goes to
-  // whichever workgroups finish first instead of a fixed, possibly slow,
-  // subset.  GEMM-2 also puts each XCD's last whole round in the pool: its
-  // tile times vary more with the expert (cold weights of small experts), and
-  // a static last round left some XCDs a tile behind the others (same box,
-  // three routings: GEMM-2 -5 to -7 us).  GEMM-1 keeps that round on its own
-  // XCD, where the 4 column tiles of a row tile share the gathered x rows in
-  // L2 (moved to the pool, they cost GEMM-1 up to 5 us).  Which workgroup
-  // computes a tile does not change its result.
-  constexpr int kPoolRounds = GEMM1 ? 0 : 1;     // whole rounds per XCD added to the pool
-  const int per_xcd = (total + 7) / 8;
-  const int xcd = blockIdx.x % 8, slot = blockIdx.x / 8, nslots = gridDim.x / 8;
-  auto xcd_lo = [&](int x) { return min(total, x * per_xcd); };
-  auto xcd_own = [&](int x) {                    // whole rounds XCD x keeps
-    return max((min(total, x * per_xcd + per_xcd) - xcd_lo(x)) / nslots - kPoolRounds, 0);
-  };
-  auto xcd_rem = [&](int x) { return min(total, x * per_xcd + per_xcd) - xcd_lo(x) - xcd_own(x) * nslots; };
-  const int x_lo = xcd_lo(xcd);
-  const int n_priv = xcd_own(xcd);
-  int pool_size = 0;
-  for (int x = 0; x < 8; ++x) pool_size += xcd_rem(x);
-  pool_size = __builtin_amdgcn_readfirstlane(pool_size);
-  auto pool_tile = [&](int g) {                  // g < pool_size
-    int x = 0;
-    for (; x < 7; ++x) {
-      const int r = xcd_rem(x);
-      if (g < r) break;
-      g -= r;
-    }
-    return min(total, x * per_xcd + per_xcd) - xcd_rem(x) + g;
-  };
-  int* const queue = p.tile_queue;               // [0]: pool items taken, [1]: workgroups done
+  const int RT = __builtin_amdgcn_readfirstlane(s_prefix[nl]);
 
-  // row0 .. row0+255: the rows a tile computes (loads clamp to row_end - 1);
-  // rows at or past valid_end are not stored; waves with wm >= act_wm compute
-  // nothing.  A tile with at most 128 rows (an expert's last, partial one) is
-  // a row half: the 4 waves of rows 0..127, one per SIMD, compute it, and a
-  // row half sums every output element in the same order as a whole tile.
-  struct Tile { int e, slot, row0, row_end, valid_end, nt, act_wm; };
-  auto decode_tile = [&](int lt) {
-    int lo = 0, hi = nl - 1;                       // largest j with s_prefix[j] <= lt
+  // ---- queues ---------------------------------------------------------------------
+  // Queue qq holds row tiles [lo(qq), lo(qq + 1)); a workgroup starts on its
+  // XCD's queue and, when that is drained, takes tiles from the others.
+  const int nq = p.n_queues;
+  const int q = __builtin_amdgcn_readfirstlane(xcc_id() & (nq - 1));
+  constexpr int kPerRowMode = MODE == kModeGateUp ? 1 : (MODE == kModeDown ? 2 : 3);
+  const int per_row = kPerRowMode == 1 ? n1 : (kPerRowMode == 2 ? n2 : n1 + n2);
+  auto q_lo = [&](int qq) { return static_cast<int>(static_cast<int64_t>(RT) * qq / nq); };
+  auto q_items = [&](int qq) { return (q_lo(qq + 1) - q_lo(qq)) * per_row; };
+
+  // Item `pos` of the queue -> tile.  g1: a GEMM-1 tile; R: global row tile;
+  // nt: column tile.  The row tile's expert is the largest j with
+  // s_prefix[j] <= R.  act_wm: waves with wm >= act_wm compute nothing (a
+  // row tile of at most 128 rows, an expert's last, runs on the 4 waves of
+  // rows 0..127, one per SIMD, and sums every output element in the same
+  // order as a whole tile).
+  struct Tile { int g1, e, slot, row0, row_end, nt, act_wm, R; };
+  auto decode = [&](int pos, int qq) {
+    const int r_lo = q_lo(qq), nr = q_lo(qq + 1) - r_lo;
+    int g1, R, c;
+    if constexpr (!BOTH) {
+      g1 = MODE == kModeGateUp;
+    } else {
+      g1 = pos < nr * n1;
+      if (!g1) pos -= nr * n1;
+    }
+    const int w = g1 ? n1 : n2;
+    R = pos / w;
+    c = pos - R * w;
+    R += r_lo;
+    int lo = 0, hi = nl - 1;
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
-      if (s_prefix[mid] <= lt) lo = mid; else hi = mid - 1;
+      if (s_prefix[mid] <= R) lo = mid; else hi = mid - 1;
     }
-    const int u = lt - s_prefix[lo];
     Tile t;                                        // uniform: keep it in SGPRs
+    t.g1 = __builtin_amdgcn_readfirstlane(g1);
     t.e = __builtin_amdgcn_readfirstlane(lo);
     t.slot = __builtin_amdgcn_readfirstlane(s_slot[lo]);
-    t.row0 = __builtin_amdgcn_readfirstlane(s_off[lo] + (u / p.n_tiles_n) * BM);
+    t.row0 = __builtin_amdgcn_readfirstlane(s_off[lo] + (R - s_prefix[lo]) * BM);
     t.row_end = __builtin_amdgcn_readfirstlane(s_off[lo + 1]);
-    t.nt = __builtin_amdgcn_readfirstlane(u % p.n_tiles_n);
-    t.valid_end = t.row_end;
+    t.nt = __builtin_amdgcn_readfirstlane(c);
+    t.R = __builtin_amdgcn_readfirstlane(R);
     t.act_wm = (t.row_end - t.row0 <= BM / 2) ? 2 : 4;
     return t;
   };
-  // item i of this workgroup: a tile of its own rounds, or pool item g
-  auto decode = [&](int i, int g) { return decode_tile(i < n_priv ? x_lo + slot + i * nslots : pool_tile(g)); };
+  // thread 0: until row tile R's GEMM-1 tiles are all counted (bounded)
+  auto wait_rows = [&](int R) {
+    int polls = 0;
+    while (atomic_read(sched + sched::kRowDone + R) < n1) {
+      if (++polls == sched::kWaitLimit) {
+        atomic_or_1(sched + sched::kFlags, sched::kFlagWait);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(4);
+    }
+  };
   // row map: perm[row0 .. row0 + BM) of a tile DMA'd into LDS (clamped to the
   // tile's last row, so every lane reads inside perm).  GEMM-1 gathers its A
   // rows through it, GEMM-2 scatters its output rows.
@@ -631,9 +735,19 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
   // 8 lg .. 8 lg + 7 of the group across the two fragments (16 contiguous
   // bytes of bf16 output per lane and store).
   auto pair_cols = [](int rb) { return (rb & ~31) | (((rb & 15) >> 2) << 3) | (((rb >> 4) & 1) << 2) | (rb & 3); };
+  // Weight stage rows: wave wn's fragments j < 4 read rows wn*64 + 16 j ..,
+  // fragments j >= 4 rows 128 + wn*64 + 16 (j - 4) ..  GEMM-1: rows < 128 are
+  // gate rows, rows >= 128 the matching up rows (act columns nt*128 + wn*64
+  // + pair_cols(16 j ..)).  GEMM-2: the same rows hold output columns
+  // nt*256 + wn*128 + pair_cols(16 j ..), so both read one LDS layout.
+  auto weight_row = [&](const Tile& t, int rb0) {
+    if (t.g1) return (rb0 < BN / 2 ? 0 : p.I) + t.nt * (BN / 2) + pair_cols(rb0 & (BN / 2 - 1));
+    const int l = (rb0 & 63) + (rb0 >= BN / 2 ? 64 : 0);
+    return t.nt * BN + ((rb0 & (BN / 2 - 1)) >> 6) * 128 + pair_cols(l);
+  };
   // (base, bytes) rather than a buffer resource: a struct member of type
   // __amdgpu_buffer_rsrc_t makes the host pass drop the kernel's launch stub
-  struct Src { const unsigned char* base; int bytes; uint32_t off[BPW]; int rot; };
+  struct Src { const unsigned char* base; int bytes; uint32_t off[BPW]; int rot, kd; };
   auto setup = [&](const Tile& t, int parity) {
     // recompute the per-lane row terms here instead of keeping them live across
     // the whole tile loop (hoisted, they outgrow the register budget and spill)
@@ -641,18 +755,21 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
     asm volatile("" : "+v"(lrow), "+v"(lchunk));
     int wv = wave;                             // opaque here too: no per-block constant is hoisted
     asm volatile("" : "+s"(wv));
+    const int K = t.g1 ? p.H : p.I;
     Src s;
-    s.rot = (!GEMM1 && KD % 4 == 0) ? (t.nt & 3) * (KD / 4) : 0;
+    s.kd = K / (2 * KS);
+    // GEMM-2 rotates its K order by the column tile (memory channels)
+    s.rot = (!t.g1 && s.kd % 4 == 0) ? (t.nt & 3) * (s.kd / 4) : 0;
     if (wave_a) {
-      s.base = static_cast<const unsigned char*>(p.A);
-      s.bytes = static_cast<int>(p.a_bytes);
-      // 32-bit offsets: the size checks keep A below 4 GiB
+      s.base = static_cast<const unsigned char*>(t.g1 ? p.x : p.act);
+      s.bytes = static_cast<int>(t.g1 ? p.x_bytes : p.act_bytes);
+      // 32-bit offsets: the size checks keep x and act below 4 GiB
       const uint32_t lane_off = static_cast<uint32_t>(lchunk * 16);
 #pragma unroll
       for (int i = 0; i < BPW; ++i) {
         const int r0 = (wv * BPW + i) * 8;                  // wave-uniform
         uint32_t src_row;
-        if constexpr (GEMM1) {
+        if (t.g1) {
           const uint32_t f = static_cast<uint32_t>(s_rows[parity * BM + r0 + lrow]);   // flat entry t*k + s
           src_row = p.k_magic ? (__umulhi(f, p.k_magic) >> p.k_shift) : f;
         } else {
@@ -664,20 +781,18 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
       // loads read past a zero-sized buffer, i.e. zeros, without memory traffic
       if (t.act_wm < 4 && wv * BPW * 8 >= t.act_wm * 64) s.bytes = 0;
     } else {
-      s.base = static_cast<const unsigned char*>(p.W) + static_cast<int64_t>(t.slot) * p.w_expert_stride * 2;
-      s.bytes = static_cast<int>(p.w_expert_stride * 2);
+      const int64_t stride = static_cast<int64_t>(t.g1 ? 2 * p.I : p.H) * K;   // elements per expert
+      s.base = static_cast<const unsigned char*>(t.g1 ? p.w_in : p.w_out) + static_cast<int64_t>(t.slot) * stride * 2;
+      s.bytes = static_cast<int>(stride * 2);
       // weight row of stage row rb0 + lrow (rb0 = the block's first row, a
-      // multiple of 8): pair_cols(rb0) + lane part, so the row split into a
+      // multiple of 8): weight_row(rb0) + lane part, so the row split into a
       // scalar per block and one per-lane term
       const int lp = ((lrow & 4) << 1) | (lrow & 3);
       const uint32_t lane_off = static_cast<uint32_t>((lp * K + lchunk * 8) * 2);
 #pragma unroll
       for (int i = 0; i < BPW; ++i) {
         const int rb0 = ((wv - 4) * BPW + i) * 8;          // wave-uniform
-        int wrow0;
-        if constexpr (GEMM1) wrow0 = (rb0 < BN / 2) ? t.nt * (BN / 2) + pair_cols(rb0) : p.N + t.nt * (BN / 2) + pair_cols(rb0 - BN / 2);
-        else wrow0 = t.nt * BN + pair_cols(rb0);
-        s.off[i] = static_cast<uint32_t>(wrow0 * K * 2) + lane_off;
+        s.off[i] = static_cast<uint32_t>(weight_row(t, rb0) * K * 2) + lane_off;
       }
     }
     return s;
@@ -688,7 +803,7 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
   const int lds_blk = wave_a ? wave * BPW * 1024 : BREGION + (wave - 4) * BPW * 1024;
   auto dma_blk = [&](const Src& s, int kd, int buf, int i) {
     int ke = kd + s.rot;
-    if (ke >= KD) ke -= KD;
+    if (ke >= s.kd) ke -= s.kd;
     // opaque: otherwise the 16 destinations (buffer x block) are hoisted into
     // scalar registers, which the loop does not have to spare
     int lb = lds_blk;
@@ -705,11 +820,10 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
   for (int kk = 0; kk < 2; ++kk) {
     const uint32_t cp = static_cast<uint32_t>(((4 * kk + lg) ^ (lr & 7)) << 4);
     a_base[kk] = static_cast<uint32_t>((wm * 64 + lr) * RB) + cp;
-    if constexpr (GEMM1) b_base[kk] = static_cast<uint32_t>(BREGION + (wn * 64 + lr) * RB) + cp;
-    else b_base[kk] = static_cast<uint32_t>(BREGION + (wn * 128 + lr) * RB) + cp;
+    b_base[kk] = static_cast<uint32_t>(BREGION + (wn * 64 + lr) * RB) + cp;
   }
-  // weight fragment j: GEMM-1 gate rows j < 4, up rows (128 rows further) j >= 4
-  auto b_off = [&](int j) { return GEMM1 ? (j < 4 ? j * 16 * RB : (BN / 2 + (j - 4) * 16) * RB) : j * 16 * RB; };
+  // weight fragment j: rows 16 j (j < 4) or 128 + 16 (j - 4) past the wave's first
+  auto b_off = [&](int j) { return j < 4 ? j * 16 * RB : (BN / 2 + (j - 4) * 16) * RB; };
   u32x4 fa[2][MF], fb[NF];
   f32x4 acc[MF][NF];
 
@@ -773,7 +887,7 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
     __builtin_amdgcn_s_waitcnt(kLgkmcnt0);
   };
 
-  // ---- epilogue -----------------------------------------------------------------------
+  // ---- epilogues ------------------------------------------------------------------------
   // From the accumulators: with the weight rows permuted per 32-column group
   // (pair_cols), lane (lr, lg) of the fragment pair (2 jp, 2 jp + 1) in row
   // fragment i holds 8 consecutive output columns of one row.  GEMM-1 stores
@@ -782,8 +896,6 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
   // lines through a per-wave LDS slice.  No workgroup barrier: the stores
   // drain while the next tile's MFMAs run.
   typedef uint16_t T;
-  T* const C = static_cast<T*>(p.C);
-  constexpr int CN = GEMM1 ? BN / 2 : BN;     // output columns per tile
   auto epilogue = [&](const Tile& t, int parity) {
     if (wm >= t.act_wm) return;
     // the last MFMAs' results must be written before they are read (the
@@ -799,25 +911,32 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
     int et = tid;
     asm volatile("" : "+v"(et));
     const int elr = et & 15, elg = (et >> 4) & 3;
-    const int col0 = t.nt * CN + (GEMM1 ? wn * 64 : wn * 128);          // the wave's first output column
-    if constexpr (GEMM1) {
-      const int col = col0 + elg * 8;                                     // first column of fragment pair 0
+    if (MODE == kModeGateUp || (BOTH && t.g1)) {
+      // act columns: lane (elr, elg) of fragment pair jp holds 8 of them
+      T* const C = static_cast<T*>(p.act);
+      const int col = t.nt * (BN / 2) + wn * 64 + elg * 8;                // first column of fragment pair 0
 #pragma unroll
       for (int i = 0; i < MF; ++i) {
         const int r = wm * 64 + i * 16 + elr;
-        T* const dst = C + static_cast<int64_t>(t.row0 + r) * p.N + col;
-        const bool ok = t.row0 + r < t.valid_end;
+        T* const dst = C + static_cast<int64_t>(t.row0 + r) * p.I + col;
+        const bool ok = t.row0 + r < t.row_end;
 #pragma unroll
         for (int jp = 0; jp < NF / 4; ++jp) {                               // fragment pairs (2 jp, 2 jp + 1)
           float v[8];
 #pragma unroll
           for (int h = 0; h < 2; ++h)
 #pragma unroll
-            for (int q = 0; q < 4; ++q) v[4 * h + q] = silu_f(acc[i][2 * jp + h][q]) * acc[i][2 * jp + h + NF / 2][q];
+            for (int q4 = 0; q4 < 4; ++q4)
+              v[4 * h + q4] = silu_f(acc[i][2 * jp + h][q4]) * acc[i][2 * jp + h + NF / 2][q4];
           u32x4 w;
 #pragma unroll
           for (int h = 0; h < 4; ++h) w[h] = pack_bf16x2(v[2 * h], v[2 * h + 1]);
-          if (ok) *reinterpret_cast<u32x4*>(dst + jp * 32) = w;
+          if (ok) {
+            if constexpr (BOTH)
+              store_dev_16(p.act, p.act_bytes, static_cast<uint32_t>((t.row0 + r) * p.I + col + jp * 32) * 2u, w);
+            else
+              *reinterpret_cast<u32x4*>(dst + jp * 32) = w;
+          }
         }
       }
     } else {
@@ -829,6 +948,8 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
       // which the memory system takes about twice as fast as half lines.
       // The slice is private to the wave and a wave's LDS accesses complete
       // in issue order, so no barrier or wait is needed around it.
+      T* const C = static_cast<T*>(p.y);
+      const int col0 = t.nt * BN + wn * 128;                              // the wave's first output column
       unsigned char* const stg = smem + STG + wave * STG_WAVE;
       const int lrow = (et >> 4) & 3, lchunk = et & 15;                    // read-back: row lrow (+4), chunk lchunk
 #pragma unroll
@@ -857,8 +978,8 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
             // the MALL and read once by the combine (non-temporal loads as
             // well); kept out of it, it no longer evicts act, x and the
             // weights, which this and the next layer step read again
-            if (t.row0 + r < t.valid_end)
-              __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(C + row * p.N + col0 + lchunk * 8));
+            if (t.row0 + r < t.row_end)
+              __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(C + row * p.H + col0 + lchunk * 8));
           }
           asm volatile("" ::: "memory");
         }
@@ -866,28 +987,59 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
     }
   };
 
-  // ---- persistent step loop ---------------------------------------------------------
-  // Items 0 and 1 are needed before the loop: with fewer than two own rounds
-  // they come from the pool now.  `pool_open`: no pool request of this
-  // workgroup has come back empty yet.
-  if (tid == 0) {
-    int g0 = pool_size, g1 = pool_size;
-    if (n_priv == 0) g0 = atomicAdd(queue, 1);
-    if (n_priv == 1 || (n_priv == 0 && g0 < pool_size)) g1 = atomicAdd(queue, 1);
-    s_pool[0] = g0;
-    s_pool[1] = g1;
-  }
-  __syncthreads();
-  const int g0 = __builtin_amdgcn_readfirstlane(s_pool[0]), g1 = __builtin_amdgcn_readfirstlane(s_pool[1]);
-  if (n_priv >= 1 || g0 < pool_size) {
-    Tile cur = decode(0, g0);
-    bool has_next = n_priv >= 2 || g1 < pool_size;
-    bool pool_open = has_next;
-    Tile nxt = has_next ? decode(1, g1) : cur;
+  // ---- persistent tile loop ---------------------------------------------------------
+  // Rounds: a workgroup takes two items from a queue (its own first; once
+  // that is drained, the next queue with items left) and runs the pipelined
+  // tile loop over that queue's items, requesting item i + 2 after step 0 of
+  // item i and reading the answer at its end, until the queue runs dry.
+  std::integral_constant<int, 0> S0;
+  std::integral_constant<int, 1> S1;
+  std::integral_constant<bool, false> NO;
+  std::integral_constant<bool, true> YES;
+  int n_done = 0;
+  int sig_r = -1;                                  // row tile of a GEMM-1 tile not yet counted
+  int cq = q;                                      // the queue of the items in hand
+  for (;;) {
+    // every wave waited for its stores (vmcnt(0)) before leaving the tile
+    // loop: count the last GEMM-1 tile, then take two items
+    __syncthreads();
+    if (tid == 0) {
+      if (BOTH && sig_r >= 0) atomic_add_1(sched + sched::kRowDone + sig_r, 1);
+      int a = INT_MAX, b = INT_MAX, qq = cq;
+      const int drained = atomic_read(sched + sched::kDrained);
+      for (int v = 0; v < nq; ++v) {
+        qq = (cq + v) & (nq - 1);
+        if ((drained >> qq) & 1) continue;
+        const int n = q_items(qq);
+        a = atomic_add_1(sched + sched::kQueue + qq, 1);
+        if (a < n) {
+          b = atomic_add_1(sched + sched::kQueue + qq, 1);
+          if (b >= n) atomic_or_1(sched + sched::kDrained, 1 << qq);
+          break;
+        }
+        atomic_or_1(sched + sched::kDrained, 1 << qq);
+        a = INT_MAX;
+      }
+      s_msg[0] = a;
+      s_msg[1] = b;
+      s_msg[3] = qq;
+    }
+    sig_r = -1;
+    __syncthreads();
+    const int i0 = __builtin_amdgcn_readfirstlane(s_msg[0]), i1 = __builtin_amdgcn_readfirstlane(s_msg[1]);
+    cq = __builtin_amdgcn_readfirstlane(s_msg[3]);
+    const int n_items = q_items(cq);
+    if (i0 >= n_items) break;                      // every queue is drained
+    int* const q_ctr = sched + sched::kQueue + cq;
+
+    Tile cur = decode(i0, cq);
+    bool has_next = i1 < n_items;
+    Tile nxt = has_next ? decode(i1, cq) : cur;
+    if (BOTH && !cur.g1 && tid == 0) wait_rows(cur.R);
     rowmap_dma(cur, 0);
     if (has_next) rowmap_dma(nxt, 1);
     __builtin_amdgcn_s_waitcnt(kVmcnt0);
-    lds_barrier();
+    __syncthreads();
     Src sc = setup(cur, 0);
 #pragma unroll
     for (int i = 0; i < BPW; ++i) dma_blk(sc, 0, 0, i);
@@ -896,73 +1048,122 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(GemmParams p) {
     __builtin_amdgcn_s_waitcnt(kVmcnt0);
     lds_barrier();
 
-    std::integral_constant<int, 0> S0;
-    std::integral_constant<int, 1> S1;
-    std::integral_constant<bool, false> NO;
-    std::integral_constant<bool, true> YES;
     // Invariant at a tile's start: its stages 0 and 1 are in buffers 0 and 1
     // (landed, published).  Steps are unrolled by four (two stages), so every
     // buffer index is an immediate.
     for (int it = 0;; ++it) {
       const bool act = wm < cur.act_wm;
-      // item it + 2 from the pool: requested after step 0, its answer lands
-      // before the wait at the end of step 2, goes to LDS after that step and
-      // is read by every wave at the end of this tile (barriers in between)
-      const bool grab = it + 2 >= n_priv && pool_open;
+      const int KT = (cur.g1 ? p.H : p.I) / KS;     // MFMA steps of this tile
+      // a GEMM-2 tile next: poll its row tile's counter at steps KT-8 .. KT-6
+      // (at step 0 for tiles too short for that), read it at step KT-4
+      const bool poll = BOTH && has_next && !nxt.g1;
       if (act) first_frags();
       step(S0, YES, NO, YES, sc, 0, 0, 0, act);          // step 0 (stage 0)
       // every wave is past its previous epilogue (barrier above), so the row
       // map buffer that epilogue read can take the next tile's row map; the
       // wait at the end of step 2 covers it, setup() reads it at step KT-3
       if (it > 0 && has_next) rowmap_dma(nxt, (it + 1) & 1);
-      int got = 0;
-      if (grab && tid == 0) got = atomicAdd(queue, 1);
+      // every wave waited for its stores (vmcnt(0)) before the barrier that
+      // ended step 0: the previous GEMM-1 tile's act rows are complete
+      if (BOTH && tid == 0 && sig_r >= 0) atomic_add_1(sched + sched::kRowDone + sig_r, 1);
+      sig_r = -1;
+      // item it + 2 is claimed at step KT-8 too (at step 0 in short tiles):
+      // as late as its answer can still reach every wave (through LDS and the
+      // barrier of step KT-2) by the end of this tile, so that a workgroup
+      // holds as few unstarted items as it can when the queues run dry
+      const bool early = KT - 8 < 4;
+      int got = 0, dep = 0;
+      if (tid == 0 && early) {
+        if (has_next) got = atomic_add_1(q_ctr, 1);
+        if (poll) dep = atomic_read(sched + sched::kRowDone + nxt.R);
+      }
       step(S1, NO, YES, YES, sc, 2, 0, 1, act);          // step 1: DMA stage 2 -> buffer 0
       step(S0, NO, NO, YES, sc, 0, 0, 1, act);           // step 2 (stage 1)
-      if (grab && tid == 0) s_pool[0] = got;
+      if (tid == 0 && early) {
+        s_msg[0] = got;
+        s_msg[2] = dep;
+      }
       step(S1, NO, YES, YES, sc, 3, 1, 0, act);          // step 3: DMA stage 3 -> buffer 1
       // steady state: steps k4 .. k4+3 (stages k4/2, k4/2 + 1) DMA stages k4/2 + 2, + 3
       for (int k4 = 4; k4 < KT - 4; k4 += 4) {
+        const bool late = k4 == KT - 8;
+        if (tid == 0 && late) {
+          if (has_next) got = atomic_add_1(q_ctr, 1);
+          if (poll) dep = atomic_read(sched + sched::kRowDone + nxt.R);
+        }
         step(S0, NO, NO, YES, sc, 0, 0, 0, act);
         step(S1, NO, YES, YES, sc, k4 / 2 + 2, 0, 1, act);
         step(S0, NO, NO, YES, sc, 0, 0, 1, act);
+        if (tid == 0 && late) {
+          s_msg[0] = got;
+          s_msg[2] = dep;
+        }
         step(S1, NO, YES, YES, sc, k4 / 2 + 3, 1, 0, act);
       }
       // last two stages: their odd steps DMA the next tile's stages 0 and 1.
-      // Without a next tile they re-read this tile's (in bounds, never consumed)
-      // so the code has no branch here.
+      // Without a next tile, or with a GEMM-2 tile whose rows are not ready,
+      // they re-read this tile's (in bounds, never consumed) so the code has
+      // no branch here.
       step(S0, NO, NO, YES, sc, 0, 0, 0, act);           // step KT-4
-      sc = has_next ? setup(nxt, (it + 1) & 1) : setup(cur, it & 1);
+      const bool ready = has_next && (!poll || __builtin_amdgcn_readfirstlane(s_msg[2]) >= n1);
+      sc = ready ? setup(nxt, (it + 1) & 1) : setup(cur, it & 1);
       step(S1, NO, YES, YES, sc, 0, 0, 1, act);          // step KT-3: next stage 0 -> buffer 0
       step(S0, NO, NO, YES, sc, 0, 0, 1, act);           // step KT-2
       step(S1, NO, YES, NO, sc, 1, 1, 0, act);           // step KT-1: next stage 1 -> buffer 1
       epilogue(cur, it & 1);
+      ++n_done;
+      if (BOTH && cur.g1) sig_r = cur.R;
       if (!has_next) {
         // no DMA may still be writing this workgroup's LDS when its waves end
         __builtin_amdgcn_s_waitcnt(kVmcnt0);
         break;
       }
       cur = nxt;
-      if (it + 2 < n_priv) {
-        nxt = decode(it + 2, 0);
-      } else if (grab) {
-        const int g = __builtin_amdgcn_readfirstlane(s_pool[0]);
-        has_next = pool_open = g < pool_size;
-        if (has_next) nxt = decode(it + 2, g);
-      } else {
-        has_next = false;
+      const int g = __builtin_amdgcn_readfirstlane(s_msg[0]);
+      has_next = g < n_items;
+      if (has_next) nxt = decode(g, cq);
+      else if (tid == 0) atomic_or_1(sched + sched::kDrained, 1 << cq);
+      if (!ready) {
+        // the rows of `cur` (a GEMM-2 tile) were not ready: count the tile
+        // just finished, wait between tiles, then load cur's first stages
+        __builtin_amdgcn_s_waitcnt(kVmcnt0);
+        __syncthreads();
+        if (tid == 0) {
+          if (BOTH && sig_r >= 0) atomic_add_1(sched + sched::kRowDone + sig_r, 1);
+          if (BOTH) wait_rows(cur.R);
+        }
+        sig_r = -1;
+        __syncthreads();
+        sc = setup(cur, (it + 1) & 1);
+#pragma unroll
+        for (int i = 0; i < BPW; ++i) dma_blk(sc, 0, 0, i);
+#pragma unroll
+        for (int i = 0; i < BPW; ++i) dma_blk(sc, 1, 1, i);
+        __builtin_amdgcn_s_waitcnt(kVmcnt0);
+        lds_barrier();
       }
     }
   }
-  // The pool counter returns to zero for the next launch: the last workgroup
-  // to get here resets it (every request of every workgroup has come back by
-  // then, and each workgroup arrives exactly once).
+  // Count this workgroup's items, then arrive; the count is complete
+  // (vmcnt(0)) before the arrival, so the last workgroup to arrive sees every
+  // count.  It checks that every queue was drained and returns every word it
+  // used to zero for the next launch.
   if (tid == 0) {
-    const int done = atomicAdd(queue + 1, 1);
-    if (done == static_cast<int>(gridDim.x) - 1) {
-      atomicExch(queue, 0);
-      atomicExch(queue + 1, 0);
+    atomic_add_1(sched + sched::kItems, n_done);
+    __builtin_amdgcn_s_waitcnt(kVmcnt0);
+    s_msg[3] = atomic_add_1(sched + sched::kDone, 1);
+  }
+  __syncthreads();
+  if (__builtin_amdgcn_readfirstlane(s_msg[3]) == static_cast<int>(gridDim.x) - 1) {
+    if (tid == 0) {
+      if (atomic_read(sched + sched::kItems) != RT * per_row) atomic_or_1(sched + sched::kFlags, sched::kFlagDrain);
+      for (int j = 0; j < 8; ++j) atomicExch(sched + sched::kQueue + j, 0);
+      atomicExch(sched + sched::kItems, 0);
+      atomicExch(sched + sched::kDrained, 0);
+      atomicExch(sched + sched::kDone, 0);
     }
+    if (BOTH)
+      for (int r = tid; r < RT; r += NT) atomicExch(sched + sched::kRowDone + r, 0);
   }
 }
 
@@ -1112,46 +1313,90 @@ __global__ __launch_bounds__(skinny::NT) void moe_gemm_skinny_kernel(GemmParams 
 }
 
 template <bool GEMM1>
-hipError_t launch_bf16(const GemmParams& p, int64_t max_rows, hipStream_t stream) {
-  const int n_cu = device_cu_count();
-  if (max_rows <= (GEMM1 ? skinny::kMaxEntries1 : skinny::kMaxEntries2)) {
-    // few rows per expert: stream each expert's weights once (same results)
-    const int n_cb = GEMM1 ? p.N / 64 : p.N / 128;
-    const int64_t chunks = (max_rows + 16 * skinny::MFC - 1) / (16 * skinny::MFC) + p.n_local;
-    const int64_t blocks = chunks * n_cb;
-    if (blocks == 0) return hipSuccess;
-    moe_gemm_skinny_kernel<GEMM1><<<dim3(static_cast<unsigned>(blocks)), skinny::NT, 0, stream>>>(p);
-    return hipGetLastError();
-  }
-  int64_t tiles = ((max_rows + bfk::BM - 1) / bfk::BM + p.n_local) * p.n_tiles_n;
-  if (tiles == 0) return hipSuccess;
-  int64_t grid = tiles < n_cu ? tiles : n_cu;
-  grid = (grid + 7) / 8 * 8;
-  moe_gemm_bf16_kernel<GEMM1><<<dim3(static_cast<unsigned>(grid)), bfk::NT, 0, stream>>>(p);
+hipError_t launch_skinny(const GemmParams& p, int64_t max_rows, hipStream_t stream) {
+  // few rows per expert: stream each expert's weights once (same results)
+  const int n_cb = GEMM1 ? p.N / 64 : p.N / 128;
+  const int64_t chunks = (max_rows + 16 * skinny::MFC - 1) / (16 * skinny::MFC) + p.n_local;
+  const int64_t blocks = chunks * n_cb;
+  if (blocks == 0) return hipSuccess;
+  moe_gemm_skinny_kernel<GEMM1><<<dim3(static_cast<unsigned>(blocks)), skinny::NT, 0, stream>>>(p);
   return hipGetLastError();
 }
 
-// Tile shapes: bf16 256x256 (GEMM-1: 128 gate + 128 up columns) on 8 waves
-// (4 x 2, 64 x 128 per wave, 2 waves per SIMD, no spills); fp32 128x128 on
-// 4 waves.
+// XCD queues of a device with n_cu compute units: one per 32 CUs (8 on a
+// whole MI355X), a power of two.
+int queues_for(int n_cu) {
+  int nq = n_cu / 32;
+  nq = nq < 1 ? 1 : (nq > 8 ? 8 : nq);
+  return pow2_floor(nq);
+}
+
+// One persistent workgroup per CU (at most one item's worth), a multiple of
+// the queue count so that every XCD runs the same number.
+template <int MODE>
+hipError_t launch_tiled(const MoeParams& p, int64_t max_rows, hipStream_t stream) {
+  const int n1 = p.I / (bfk::BN / 2), n2 = p.H / bfk::BN;
+  const int per_row = MODE == kModeGateUp ? n1 : (MODE == kModeDown ? n2 : n1 + n2);
+  const int64_t items = ((max_rows + bfk::BM - 1) / bfk::BM + p.n_local) * per_row;
+  if (items == 0) return hipSuccess;
+  const int nq = p.n_queues;
+  const int64_t cap = device_cu_count() / nq * nq;
+  int64_t grid = items < cap ? items : cap;
+  grid = (grid + nq - 1) / nq * nq;
+  moe_gemm_bf16_kernel<MODE><<<dim3(static_cast<unsigned>(grid)), bfk::NT, 0, stream>>>(p);
+  return hipGetLastError();
+}
+
+MoeParams moe_params(const void* x, int64_t n_tokens, int top_k, const int32_t* perm, const int32_t* offsets,
+                     int n_local, int64_t max_rows, const void* w_in, const void* w_out, const int32_t* w_slot,
+                     int hidden, int inter, void* act, void* y, int32_t* sched) {
+  MoeParams p;
+  p.x = x; p.act = act; p.y = y; p.perm = perm; p.offsets = offsets; p.w_slot = w_slot;
+  p.w_in = w_in; p.w_out = w_out;
+  p.n_local = n_local; p.top_k = top_k; p.H = hidden; p.I = inter;
+  p.x_bytes = static_cast<uint32_t>(n_tokens * hidden * 2);
+  p.act_bytes = static_cast<uint32_t>(max_rows * inter * 2);
+  div_magic(static_cast<uint32_t>(top_k), &p.k_magic, &p.k_shift);
+  p.n_queues = queues_for(device_cu_count());
+  p.sched = sched;
+  return p;
+}
+
+// The bf16 tiled kernels need K a multiple of 256 (whole four-step rounds,
+// GEMM-2's stage rotation) and more rows than the small-batch kernels take.
+bool tiled_gate_up(int dtype, int64_t max_rows) {
+  return dtype == MEP_DTYPE_BF16 && max_rows > skinny::kMaxEntries1;
+}
+bool tiled_down(int dtype, int64_t max_rows, int inter) {
+  return dtype == MEP_DTYPE_BF16 && inter % 256 == 0 && max_rows > skinny::kMaxEntries2;
+}
+
+// Tile shapes of the generic kernel (fp32, and bf16 GEMM-2 with I % 256 != 0):
+// bf16 256x256 on 8 waves (4 x 2), fp32 128x128 on 4 waves.
 typedef TileCfg<256, 256, 4, 2> CfgBf16;
 typedef TileCfg<128, 128, 2, 2> CfgF32;
 
 template <int DT, class Cfg>
 int run_gate_up(const void* x, int64_t n_tokens, int top_k, const int32_t* perm, const int32_t* offsets,
                 int n_local, int64_t max_rows, const void* w_in, const int32_t* w_slot, int hidden, int inter,
-                void* act, int32_t* tile_queue, hipStream_t stream) {
-  GemmParams g1;
-  g1.A = x; g1.perm = perm; g1.offsets = offsets; g1.W = w_in; g1.C = act; g1.tile_queue = tile_queue;
-  g1.w_slot = w_slot;
-  g1.w_expert_stride = static_cast<int64_t>(2) * inter * hidden;
-  g1.n_local = n_local; g1.top_k = top_k; g1.K = hidden; g1.N = inter;
-  g1.n_tiles_n = inter / (Cfg::BN / 2);
-  g1.a_bytes = static_cast<uint32_t>(n_tokens * hidden * dtype_bytes(DT));
-  div_magic(static_cast<uint32_t>(top_k), &g1.k_magic, &g1.k_shift);
+                void* act, int32_t* sched, hipStream_t stream) {
   hipError_t e;
-  if (DT == MEP_DTYPE_BF16 && hidden % 256 == 0) e = launch_bf16<true>(g1, max_rows, stream);
-  else e = launch<DT, Cfg, true>(g1, max_rows, stream);
+  if (tiled_gate_up(DT, max_rows)) {
+    const MoeParams p = moe_params(x, n_tokens, top_k, perm, offsets, n_local, max_rows, w_in, nullptr, w_slot,
+                                   hidden, inter, act, nullptr, sched);
+    e = launch_tiled<kModeGateUp>(p, max_rows, stream);
+  } else {
+    GemmParams g1;
+    g1.A = x; g1.perm = perm; g1.offsets = offsets; g1.W = w_in; g1.C = act;
+    g1.w_slot = w_slot;
+    g1.w_expert_stride = static_cast<int64_t>(2) * inter * hidden;
+    g1.n_local = n_local; g1.top_k = top_k; g1.K = hidden; g1.N = inter;
+    g1.n_tiles_n = inter / (Cfg::BN / 2);
+    g1.a_bytes = static_cast<uint32_t>(n_tokens * hidden * dtype_bytes(DT));
+    div_magic(static_cast<uint32_t>(top_k), &g1.k_magic, &g1.k_shift);
+    if (DT == MEP_DTYPE_BF16) e = launch_skinny<true>(g1, max_rows, stream);
+    else e = launch<DT, Cfg, true>(g1, max_rows, stream);
+  }
   MEP_REQUIRE(e == hipSuccess, MEP_ERR_HIP, "mep_swiglu_gate_up: %s", hipGetErrorString(e));
   return MEP_OK;
 }
@@ -1159,18 +1404,24 @@ int run_gate_up(const void* x, int64_t n_tokens, int top_k, const int32_t* perm,
 template <int DT, class Cfg>
 int run_down(const void* act, int top_k, const int32_t* perm, const int32_t* offsets, int n_local,
              int64_t max_rows, const void* w_out, const int32_t* w_slot, int hidden, int inter, void* y,
-             int32_t* tile_queue, hipStream_t stream) {
-  GemmParams g2;
-  g2.A = act; g2.perm = perm; g2.offsets = offsets; g2.W = w_out; g2.C = y; g2.tile_queue = tile_queue;
-  g2.w_slot = w_slot;
-  g2.w_expert_stride = static_cast<int64_t>(hidden) * inter;
-  g2.n_local = n_local; g2.top_k = top_k; g2.K = inter; g2.N = hidden;
-  g2.n_tiles_n = hidden / Cfg::BN;
-  g2.a_bytes = static_cast<uint32_t>(max_rows * inter * dtype_bytes(DT));
-  div_magic(static_cast<uint32_t>(top_k), &g2.k_magic, &g2.k_shift);
+             int32_t* sched, hipStream_t stream) {
   hipError_t e;
-  if (DT == MEP_DTYPE_BF16 && inter % 256 == 0) e = launch_bf16<false>(g2, max_rows, stream);
-  else e = launch<DT, Cfg, false>(g2, max_rows, stream);
+  if (tiled_down(DT, max_rows, inter)) {
+    MoeParams p = moe_params(nullptr, 0, top_k, perm, offsets, n_local, max_rows, nullptr, w_out, w_slot, hidden,
+                             inter, const_cast<void*>(act), y, sched);
+    e = launch_tiled<kModeDown>(p, max_rows, stream);
+  } else {
+    GemmParams g2;
+    g2.A = act; g2.perm = perm; g2.offsets = offsets; g2.W = w_out; g2.C = y;
+    g2.w_slot = w_slot;
+    g2.w_expert_stride = static_cast<int64_t>(hidden) * inter;
+    g2.n_local = n_local; g2.top_k = top_k; g2.K = inter; g2.N = hidden;
+    g2.n_tiles_n = hidden / Cfg::BN;
+    g2.a_bytes = static_cast<uint32_t>(max_rows * inter * dtype_bytes(DT));
+    div_magic(static_cast<uint32_t>(top_k), &g2.k_magic, &g2.k_shift);
+    if (DT == MEP_DTYPE_BF16 && inter % 256 == 0) e = launch_skinny<false>(g2, max_rows, stream);
+    else e = launch<DT, Cfg, false>(g2, max_rows, stream);
+  }
   MEP_REQUIRE(e == hipSuccess, MEP_ERR_HIP, "mep_swiglu_down: %s", hipGetErrorString(e));
   return MEP_OK;
 }
@@ -1207,14 +1458,29 @@ using namespace mep;
 namespace mep {
 namespace {
 
+// The schedule buffer a launch needs: non-null, and at least
+// mep_experts_queue_ints(max_rows, n_local) words when a tiled kernel runs.
+int check_queue(const char* fn, bool tiled, int32_t* tile_queue, size_t tile_queue_ints, int64_t max_rows,
+                int n_local) {
+  MEP_REQUIRE(tile_queue != nullptr, MEP_ERR_INVALID_ARG, "%s: null tile_queue", fn);
+  if (tiled) {
+    const int64_t need = sched::words(max_rows, n_local);
+    MEP_REQUIRE(static_cast<int64_t>(tile_queue_ints) >= need, MEP_ERR_WORKSPACE,
+                "%s: tile_queue has %zu ints < required %lld", fn, tile_queue_ints, (long long)need);
+  }
+  return MEP_OK;
+}
+
 int gate_up_impl(const char* fn, const void* x, int64_t n_tokens, int32_t top_k, const int32_t* perm,
                  const int32_t* offsets, int32_t n_local, int64_t max_rows, const void* w_in,
                  const int32_t* w_slot, int32_t hidden, int32_t inter, int32_t dtype, void* act,
-                 size_t act_bytes, int32_t* tile_queue, void* stream) {
+                 size_t act_bytes, int32_t* tile_queue, size_t tile_queue_ints, void* stream) {
   int rc = check_expert_args(fn, n_tokens, top_k, n_local, max_rows, hidden, inter, dtype);
   if (rc != MEP_OK) return rc;
   if (max_rows == 0 || n_local == 0) return MEP_OK;
-  MEP_REQUIRE(x && perm && offsets && w_in && act && tile_queue, MEP_ERR_INVALID_ARG, "%s: null pointer", fn);
+  MEP_REQUIRE(x && perm && offsets && w_in && act, MEP_ERR_INVALID_ARG, "%s: null pointer", fn);
+  rc = check_queue(fn, tiled_gate_up(dtype, max_rows), tile_queue, tile_queue_ints, max_rows, n_local);
+  if (rc != MEP_OK) return rc;
   const size_t need = static_cast<size_t>(max_rows) * inter * dtype_bytes(dtype);
   MEP_REQUIRE(act_bytes >= need, MEP_ERR_WORKSPACE, "%s: act %zu B < required %zu B", fn, act_bytes, need);
   MEP_REQUIRE(aligned16(x) && aligned16(w_in) && aligned16(act), MEP_ERR_INVALID_ARG,
@@ -1229,12 +1495,14 @@ int gate_up_impl(const char* fn, const void* x, int64_t n_tokens, int32_t top_k,
 
 int down_impl(const char* fn, const void* act, int64_t n_tokens, int32_t top_k, const int32_t* perm,
               const int32_t* offsets, int32_t n_local, int64_t max_rows, const void* w_out, const int32_t* w_slot,
-              int32_t hidden, int32_t inter, int32_t dtype, void* y_entries, int32_t* tile_queue, void* stream) {
+              int32_t hidden, int32_t inter, int32_t dtype, void* y_entries, int32_t* tile_queue,
+              size_t tile_queue_ints, void* stream) {
   int rc = check_expert_args(fn, n_tokens, top_k, n_local, max_rows, hidden, inter, dtype);
   if (rc != MEP_OK) return rc;
   if (max_rows == 0 || n_local == 0) return MEP_OK;
-  MEP_REQUIRE(act && perm && offsets && w_out && y_entries && tile_queue, MEP_ERR_INVALID_ARG,
-              "%s: null pointer", fn);
+  MEP_REQUIRE(act && perm && offsets && w_out && y_entries, MEP_ERR_INVALID_ARG, "%s: null pointer", fn);
+  rc = check_queue(fn, tiled_down(dtype, max_rows, inter), tile_queue, tile_queue_ints, max_rows, n_local);
+  if (rc != MEP_OK) return rc;
   MEP_REQUIRE(aligned16(act) && aligned16(w_out) && aligned16(y_entries), MEP_ERR_INVALID_ARG,
               "%s: buffers must be 16-byte aligned", fn);
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -1245,10 +1513,13 @@ int down_impl(const char* fn, const void* act, int64_t n_tokens, int32_t top_k, 
                                          inter, y_entries, tile_queue, s);
 }
 
+// Both GEMMs: one launch of the tiled kernel when both would run tiled, else
+// the two launches.
 int grouped_impl(const char* fn, const void* x, int64_t n_tokens, int32_t top_k, const int32_t* perm,
                  const int32_t* offsets, int32_t n_local, int64_t max_rows, const void* w_in, const void* w_out,
                  const int32_t* w_slot, int32_t hidden, int32_t inter, int32_t dtype, void* y_entries,
-                 void* workspace, size_t workspace_bytes, int32_t* tile_queue, void* stream) {
+                 void* workspace, size_t workspace_bytes, int32_t* tile_queue, size_t tile_queue_ints,
+                 void* stream) {
   int rc = check_expert_args(fn, n_tokens, top_k, n_local, max_rows, hidden, inter, dtype);
   if (rc != MEP_OK) return rc;
   if (max_rows == 0 || n_local == 0) return MEP_OK;
@@ -1256,33 +1527,65 @@ int grouped_impl(const char* fn, const void* x, int64_t n_tokens, int32_t top_k,
   const size_t need = mep_experts_workspace_size(max_rows, inter, dtype);
   MEP_REQUIRE(workspace_bytes >= need, MEP_ERR_WORKSPACE, "%s: workspace %zu B < required %zu B", fn,
               workspace_bytes, need);
+  if (tiled_gate_up(dtype, max_rows) && tiled_down(dtype, max_rows, inter)) {
+    MEP_REQUIRE(x && perm && offsets && w_in && w_out && y_entries, MEP_ERR_INVALID_ARG, "%s: null pointer", fn);
+    rc = check_queue(fn, true, tile_queue, tile_queue_ints, max_rows, n_local);
+    if (rc != MEP_OK) return rc;
+    MEP_REQUIRE(aligned16(x) && aligned16(w_in) && aligned16(w_out) && aligned16(workspace) && aligned16(y_entries),
+                MEP_ERR_INVALID_ARG, "%s: buffers must be 16-byte aligned", fn);
+    const MoeParams p = moe_params(x, n_tokens, top_k, perm, offsets, n_local, max_rows, w_in, w_out, w_slot,
+                                   hidden, inter, workspace, y_entries, tile_queue);
+    const hipError_t e = launch_tiled<kModeBoth>(p, max_rows, static_cast<hipStream_t>(stream));
+    MEP_REQUIRE(e == hipSuccess, MEP_ERR_HIP, "%s: %s", fn, hipGetErrorString(e));
+    return MEP_OK;
+  }
   rc = gate_up_impl(fn, x, n_tokens, top_k, perm, offsets, n_local, max_rows, w_in, w_slot, hidden, inter, dtype,
-                    workspace, workspace_bytes, tile_queue, stream);
+                    workspace, workspace_bytes, tile_queue, tile_queue_ints, stream);
   if (rc != MEP_OK) return rc;
   return down_impl(fn, workspace, n_tokens, top_k, perm, offsets, n_local, max_rows, w_out, w_slot, hidden, inter,
-                   dtype, y_entries, tile_queue, stream);
+                   dtype, y_entries, tile_queue, tile_queue_ints, stream);
 }
 
 }  // namespace
 }  // namespace mep
 
+extern "C" size_t mep_experts_queue_ints(int64_t max_rows, int32_t n_local) {
+  if (max_rows < 0 || n_local < 0) return 0;
+  return static_cast<size_t>(mep::sched::words(max_rows, n_local));
+}
+
+extern "C" int mep_experts_check(const int32_t* tile_queue, void* stream) {
+  clear_error();
+  MEP_REQUIRE(tile_queue != nullptr, MEP_ERR_INVALID_ARG, "mep_experts_check: null tile_queue");
+  hipError_t e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
+  MEP_REQUIRE(e == hipSuccess, MEP_ERR_HIP, "mep_experts_check: %s", hipGetErrorString(e));
+  int32_t flags = 0;
+  e = hipMemcpy(&flags, tile_queue + mep::sched::kFlags, sizeof(flags), hipMemcpyDeviceToHost);
+  MEP_REQUIRE(e == hipSuccess, MEP_ERR_HIP, "mep_experts_check: %s", hipGetErrorString(e));
+  MEP_REQUIRE(!(flags & mep::sched::kFlagWait), MEP_ERR_HIP,
+              "mep_experts_check: a GEMM-2 tile gave up waiting for its GEMM-1 rows (results invalid)");
+  MEP_REQUIRE(!(flags & mep::sched::kFlagDrain), MEP_ERR_HIP,
+              "mep_experts_check: a tile queue was not drained (results invalid)");
+  return MEP_OK;
+}
+
 extern "C" int mep_swiglu_gate_up(const void* x, int64_t n_tokens, int32_t top_k,
                                   const int32_t* perm, const int32_t* offsets, int32_t n_local,
                                   int64_t max_rows, const void* w_in, int32_t hidden, int32_t inter,
                                   int32_t dtype, void* act, size_t act_bytes, int32_t* tile_queue,
-                                  void* stream) {
+                                  size_t tile_queue_ints, void* stream) {
   clear_error();
   return gate_up_impl("mep_swiglu_gate_up", x, n_tokens, top_k, perm, offsets, n_local, max_rows, w_in, nullptr,
-                      hidden, inter, dtype, act, act_bytes, tile_queue, stream);
+                      hidden, inter, dtype, act, act_bytes, tile_queue, tile_queue_ints, stream);
 }
 
 extern "C" int mep_swiglu_down(const void* act, int64_t n_tokens, int32_t top_k, const int32_t* perm,
                                const int32_t* offsets, int32_t n_local, int64_t max_rows,
                                const void* w_out, int32_t hidden, int32_t inter, int32_t dtype,
-                               void* y_entries, int32_t* tile_queue, void* stream) {
+                               void* y_entries, int32_t* tile_queue, size_t tile_queue_ints, void* stream) {
   clear_error();
   return down_impl("mep_swiglu_down", act, n_tokens, top_k, perm, offsets, n_local, max_rows, w_out, nullptr,
-                   hidden, inter, dtype, y_entries, tile_queue, stream);
+                   hidden, inter, dtype, y_entries, tile_queue, tile_queue_ints, stream);
 }
 
 extern "C" size_t mep_experts_workspace_size(int64_t max_rows, int32_t inter, int32_t dtype) {
@@ -1296,10 +1599,11 @@ extern "C" int mep_grouped_swiglu(const void* x, int64_t n_tokens, int32_t top_k
                                   int64_t max_rows, const void* w_in, const void* w_out,
                                   int32_t hidden, int32_t inter, int32_t dtype, void* y_entries,
                                   void* workspace, size_t workspace_bytes, int32_t* tile_queue,
-                                  void* stream) {
+                                  size_t tile_queue_ints, void* stream) {
   clear_error();
   return grouped_impl("mep_grouped_swiglu", x, n_tokens, top_k, perm, offsets, n_local, max_rows, w_in, w_out,
-                      nullptr, hidden, inter, dtype, y_entries, workspace, workspace_bytes, tile_queue, stream);
+                      nullptr, hidden, inter, dtype, y_entries, workspace, workspace_bytes, tile_queue,
+                      tile_queue_ints, stream);
 }
 
 extern "C" int mep_grouped_swiglu_slots(const void* x, int64_t n_tokens, int32_t top_k,
@@ -1307,11 +1611,11 @@ extern "C" int mep_grouped_swiglu_slots(const void* x, int64_t n_tokens, int32_t
                                         int64_t max_rows, const void* w_in, const void* w_out,
                                         const int32_t* w_slot, int32_t hidden, int32_t inter, int32_t dtype,
                                         void* y_entries, void* workspace, size_t workspace_bytes,
-                                        int32_t* tile_queue, void* stream) {
+                                        int32_t* tile_queue, size_t tile_queue_ints, void* stream) {
   clear_error();
   MEP_REQUIRE(w_slot != nullptr || n_local == 0 || max_rows == 0, MEP_ERR_INVALID_ARG,
               "mep_grouped_swiglu_slots: null w_slot");
   return grouped_impl("mep_grouped_swiglu_slots", x, n_tokens, top_k, perm, offsets, n_local, max_rows, w_in,
                       w_out, w_slot, hidden, inter, dtype, y_entries, workspace, workspace_bytes, tile_queue,
-                      stream);
+                      tile_queue_ints, stream);
 }

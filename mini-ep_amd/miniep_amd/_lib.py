@@ -74,19 +74,22 @@ _SIGNATURES = {
                                             _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                             _c_void_p, _c_void_p, _c_void_p]),
     "mep_experts_workspace_size": (_size, [_i64, _i32, _i32]),
+    "mep_experts_queue_ints": (_size, [_i64, _i32]),
+    "mep_experts_check": (ctypes.c_int, [_c_void_p, _c_void_p]),
     "mep_grouped_swiglu": (ctypes.c_int, [_c_void_p, _i64, _i32, _c_void_p, _c_void_p, _i32,
                                           _i64, _c_void_p, _c_void_p, _i32, _i32, _i32,
-                                          _c_void_p, _c_void_p, _size, _c_void_p, _c_void_p]),
+                                          _c_void_p, _c_void_p, _size, _c_void_p, _size, _c_void_p]),
     "mep_grouped_swiglu_slots": (ctypes.c_int, [_c_void_p, _i64, _i32, _c_void_p, _c_void_p, _i32,
                                                 _i64, _c_void_p, _c_void_p, _c_void_p, _i32, _i32, _i32,
-                                                _c_void_p, _c_void_p, _size, _c_void_p, _c_void_p]),
+                                                _c_void_p, _c_void_p, _size, _c_void_p, _size, _c_void_p]),
     "mep_copy_experts": (ctypes.c_int, [_c_void_p, _c_void_p, _i32, _c_void_p, _c_void_p, _i32,
                                         ctypes.POINTER(_i32), ctypes.POINTER(_i32), _i32, _i32, _i32, _i32,
                                         _c_void_p]),
     "mep_swiglu_gate_up": (ctypes.c_int, [_c_void_p, _i64, _i32, _c_void_p, _c_void_p, _i32, _i64,
-                                          _c_void_p, _i32, _i32, _i32, _c_void_p, _size, _c_void_p, _c_void_p]),
+                                          _c_void_p, _i32, _i32, _i32, _c_void_p, _size, _c_void_p, _size,
+                                          _c_void_p]),
     "mep_swiglu_down": (ctypes.c_int, [_c_void_p, _i64, _i32, _c_void_p, _c_void_p, _i32, _i64,
-                                       _c_void_p, _i32, _i32, _i32, _c_void_p, _c_void_p, _c_void_p]),
+                                       _c_void_p, _i32, _i32, _i32, _c_void_p, _c_void_p, _size, _c_void_p]),
     "mep_combine": (ctypes.c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i32,
                                    _i32, _i32, _c_void_p, _c_void_p]),
     "mep_gather_rows": (ctypes.c_int, [_c_void_p, _i64, _i32, _c_void_p, _i64, _i32, _i32, _c_void_p,

@@ -49,15 +49,29 @@ def _stream(dev: torch.device) -> int:
 _QUEUES: dict[tuple[int, int], torch.Tensor] = {}
 
 
-def _tile_queue(dev: torch.device) -> torch.Tensor:
-    """Tile-queue counters of the grouped GEMMs for the current stream of
-    ``dev``: zeroed once here, left at zero by every launch, and one per stream
-    so that launches on different streams never share counters."""
+def _tile_queue(dev: torch.device, max_rows: int, n_local: int) -> torch.Tensor:
+    """Schedule buffer of the tiled grouped GEMMs for the current stream of
+    ``dev`` (mep_experts_queue_ints words): zeroed here, left at zero by
+    every launch (but for its sticky error word, see ``experts_check``), one
+    per stream so that launches on different streams never share it, and
+    replaced by a larger zeroed one when a launch needs more words."""
+    key = (dev.index if dev.index is not None else torch.cuda.current_device(), _stream(dev))
+    need = int(_lib.lib().mep_experts_queue_ints(max_rows, n_local))
+    q = _QUEUES.get(key)
+    if q is None or q.numel() < need:
+        q = _QUEUES[key] = torch.zeros(max(need, 64), dtype=torch.int32, device=dev)
+    return q
+
+
+def experts_check(dev: torch.device | None = None) -> None:
+    """Synchronise and raise MepError if a grouped-GEMM launch on the current
+    stream of ``dev`` flagged its results invalid (a GEMM-2 tile that gave
+    up waiting for its GEMM-1 rows, or a tile queue nobody drained)."""
+    dev = dev or torch.device("cuda", torch.cuda.current_device())
     key = (dev.index if dev.index is not None else torch.cuda.current_device(), _stream(dev))
     q = _QUEUES.get(key)
-    if q is None:
-        q = _QUEUES[key] = torch.zeros(2, dtype=torch.int32, device=dev)
-    return q
+    if q is not None:
+        _lib.check(_lib.lib().mep_experts_check(q.data_ptr(), _stream(dev)), "mep_experts_check")
 
 
 def _mask_u8(valid_mask: torch.Tensor | None, n: int) -> torch.Tensor | None:
@@ -256,10 +270,11 @@ def grouped_swiglu(x_flat: torch.Tensor, disp: Dispatch, w_in: torch.Tensor, w_o
     max_rows = n * disp.top_k
     ws_bytes = L.mep_experts_workspace_size(max_rows, inter, code)
     ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
+    tq = _tile_queue(dev, max_rows, disp.n_local)
     if w_slot is None:
         rc = L.mep_grouped_swiglu(x.data_ptr(), n, disp.top_k, disp.perm.data_ptr(), disp.offsets.data_ptr(),
                                   disp.n_local, max_rows, wi.data_ptr(), wo.data_ptr(), h, inter, code,
-                                  y_entries.data_ptr(), ws.data_ptr(), ws.numel(), _tile_queue(dev).data_ptr(),
+                                  y_entries.data_ptr(), ws.data_ptr(), ws.numel(), tq.data_ptr(), tq.numel(),
                                   _stream(dev))
         _lib.check(rc, "mep_grouped_swiglu")
     else:
@@ -267,7 +282,7 @@ def grouped_swiglu(x_flat: torch.Tensor, disp: Dispatch, w_in: torch.Tensor, w_o
                                         disp.offsets.data_ptr(), disp.n_local, max_rows, wi.data_ptr(),
                                         wo.data_ptr(), w_slot.contiguous().data_ptr(), h, inter, code,
                                         y_entries.data_ptr(), ws.data_ptr(), ws.numel(),
-                                        _tile_queue(dev).data_ptr(), _stream(dev))
+                                        tq.data_ptr(), tq.numel(), _stream(dev))
         _lib.check(rc, "mep_grouped_swiglu_slots")
     return y_entries
 
@@ -317,10 +332,11 @@ def swiglu_gate_up(x_flat: torch.Tensor, disp: Dispatch, w_in: torch.Tensor,
     if act is None:
         act = torch.empty((max(n * disp.top_k, 1), inter), dtype=x.dtype, device=dev)
     wi = w_in.to(x.dtype).contiguous()
+    tq = _tile_queue(dev, n * disp.top_k, disp.n_local)
     rc = _lib.lib().mep_swiglu_gate_up(x.data_ptr(), n, disp.top_k, disp.perm.data_ptr(),
                                        disp.offsets.data_ptr(), disp.n_local, n * disp.top_k,
                                        wi.data_ptr(), h, inter, _dtype_code(x), act.data_ptr(),
-                                       act.numel() * act.element_size(), _tile_queue(dev).data_ptr(),
+                                       act.numel() * act.element_size(), tq.data_ptr(), tq.numel(),
                                        _stream(dev))
     _lib.check(rc, "mep_swiglu_gate_up")
     return act
@@ -334,10 +350,11 @@ def swiglu_down(act: torch.Tensor, x_flat: torch.Tensor, disp: Dispatch, w_out: 
     if y_entries is None:
         y_entries = torch.empty((max(n * disp.top_k, 1), h), dtype=act.dtype, device=dev)
     wo = w_out.to(act.dtype).contiguous()
+    tq = _tile_queue(dev, n * disp.top_k, disp.n_local)
     rc = _lib.lib().mep_swiglu_down(act.data_ptr(), n, disp.top_k, disp.perm.data_ptr(),
                                     disp.offsets.data_ptr(), disp.n_local, n * disp.top_k, wo.data_ptr(),
                                     h, inter, _dtype_code(act), y_entries.data_ptr(),
-                                    _tile_queue(dev).data_ptr(), _stream(dev))
+                                    tq.data_ptr(), tq.numel(), _stream(dev))
     _lib.check(rc, "mep_swiglu_down")
     return y_entries
 

@@ -42,11 +42,12 @@ def _moe_layer_raw(L, x, w_r, w_in, w_out, k=8):
     ok(L.mep_dispatch_check(ws.data_ptr(), s))
     act = torch.empty(L.mep_experts_workspace_size(N * k, I, BF16), dtype=torch.uint8, device="cuda")
     y = torch.empty(N * k, H, dtype=x.dtype, device="cuda")
-    queue = torch.zeros(2, dtype=torch.int32, device="cuda")
+    queue = torch.zeros(L.mep_experts_queue_ints(N * k, E), dtype=torch.int32, device="cuda")
     ok(L.mep_grouped_swiglu(x.data_ptr(), N, k, perm.data_ptr(), offsets.data_ptr(), E, N * k, w_in.data_ptr(),
                             w_out.data_ptr(), H, I, BF16, y.data_ptr(), act.data_ptr(), act.numel(),
-                            queue.data_ptr(), s))
-    assert queue.tolist() == [0, 0]                      # every launch leaves the tile queue at zero
+                            queue.data_ptr(), queue.numel(), s))
+    ok(L.mep_experts_check(queue.data_ptr(), s))
+    assert int(queue.abs().sum()) == 0                   # every launch leaves the schedule words at zero
     out = torch.empty(N, H, dtype=x.dtype, device="cuda")
     ok(L.mep_combine(y.data_ptr(), gate.data_ptr(), row.data_ptr(), None, N, k, H, BF16, out.data_ptr(), s))
     return out, idx, gate
@@ -79,6 +80,18 @@ def test_error_codes_and_messages():
     rc = L.mep_combine(None, None, None, None, 4, 8, 1024, 1, None, None)
     assert rc == _lib.ERR_INVALID_ARG
     rc = L.mep_grouped_swiglu(x.data_ptr(), 4, 8, x.data_ptr(), x.data_ptr(), 4, 32, x.data_ptr(), x.data_ptr(),
-                              1024, 512, 1, x.data_ptr(), x.data_ptr(), 16, x.data_ptr(), None)
+                              1024, 512, 1, x.data_ptr(), x.data_ptr(), 16, x.data_ptr(), 64, None)
     assert rc == _lib.ERR_WORKSPACE
-    assert L.mep_abi_version() == 2
+    # a tiled launch needs mep_experts_queue_ints words of schedule (checked before anything is enqueued)
+    big = torch.zeros(9 << 20, dtype=torch.int32, device="cuda")     # 36 MiB: covers act of 32768 rows
+    need = L.mep_experts_queue_ints(4096 * 8, 32)
+    assert need == 16 + 4096 * 8 // 256 + 32
+    rc = L.mep_grouped_swiglu(big.data_ptr(), 4096, 8, big.data_ptr(), big.data_ptr(), 32, 4096 * 8, big.data_ptr(),
+                              big.data_ptr(), 1024, 512, 1, big.data_ptr(), big.data_ptr(), big.numel() * 4,
+                              big.data_ptr(), need - 1, None)
+    assert rc == _lib.ERR_WORKSPACE and b"tile_queue" in L.mep_last_error()
+    rc = L.mep_grouped_swiglu(big.data_ptr(), 4096, 8, big.data_ptr(), big.data_ptr(), 32, 4096 * 8, big.data_ptr(),
+                              big.data_ptr(), 1024, 512, 1, big.data_ptr(), big.data_ptr(), big.numel() * 4,
+                              None, need, None)
+    assert rc == _lib.ERR_INVALID_ARG
+    assert L.mep_abi_version() == 3

@@ -123,9 +123,9 @@ def test_errors():
 
 
 def test_tile_queue_two_streams_and_repeats():
-    """The bf16 GEMMs hand out their last round of tiles through a per-stream
-    counter pair: launches on two streams at once and many launches in a row
-    give the serial result bit for bit, and leave every counter at zero."""
+    """The tiled bf16 GEMMs schedule their tiles through a per-stream buffer
+    of counters: launches on two streams at once and many launches in a row
+    give the serial result bit for bit, and leave every word at zero."""
     banner("experts tile queue")
     outs = []
     cases = []
@@ -150,8 +150,73 @@ def test_tile_queue_two_streams_and_repeats():
         torch.cuda.synchronize()
         for y, r in zip(ys, ref):
             assert torch.equal(y, r)
+    ops.experts_check()
     for q in ops._QUEUES.values():
-        assert q.tolist() == [0, 0]
+        assert int(q.abs().sum()) == 0
+
+
+def _two_launches(x, d, w_in, w_out, y):
+    act = ops.swiglu_gate_up(x, d, w_in)
+    return ops.swiglu_down(act, x, d, w_out, y)
+
+
+@pytest.mark.parametrize("case", ["zipf_t16384", "tiny_t300", "ragged_e16", "e64_masked", "zipf_t40000"])
+def test_one_launch_equals_two_launches(case):
+    """bf16 with more than 2048 entries runs both GEMMs as one launch (each
+    XCD's row tiles, GEMM-2 tiles waiting for their GEMM-1 rows).  It must
+    give the two separate launches' bits on every dispatched row, leave the
+    other rows alone, leave the schedule words at zero and flag nothing:
+    many row tiles per XCD (the interleaved order), fewer row tiles than the
+    lag (GEMM-1 first, then GEMM-2), ragged counts with empty experts and
+    row halves, 64 experts with masked tokens."""
+    banner(f"experts one launch vs two: {case}")
+    bf = torch.bfloat16
+    valid = None
+    if case.startswith("zipf"):
+        T = int(case.split("_t")[1])
+        L = workloads.make_layer(T, seed=11, zipf_s=1.2)
+        topk = (L.x @ L.w_router.T).topk(8, dim=-1).indices
+        x, w_in, w_out = L.x, L.w_in, L.w_out
+    elif case == "tiny_t300":
+        g = torch.Generator().manual_seed(12)
+        topk = torch.rand(300, 32, generator=g).topk(8, -1).indices
+        x = torch.randn(300, 1024, generator=g)
+        w_in, w_out = workloads.expert_weights(g, 32)
+    elif case == "ragged_e16":
+        counts = [0, 1, 129, 256, 257, 6000, 6000, 5000, 3000, 2000, 1000, 357, 0, 0, 0, 0]
+        topk = _topk_with_counts(counts, 4, 6000, 13)
+        g = torch.Generator().manual_seed(13)
+        x = torch.randn(6000, 1024, generator=g)
+        w_in, w_out = workloads.expert_weights(g, 16)
+    else:
+        g = torch.Generator().manual_seed(14)
+        topk = torch.rand(3000, 64, generator=g).topk(8, -1).indices
+        valid = torch.rand(3000, generator=g) < 0.6
+        x = torch.randn(3000, 1024, generator=g)
+        w_in, w_out = workloads.expert_weights(g, 64)
+    n, k = topk.shape
+    E = w_in.shape[0]
+    table, n_rep, g2l = _world1(E)
+    d = ops.dispatch(topk.to(DEV), None if valid is None else valid.to(DEV), E, table, n_rep, False, None, 0, g2l, E)
+    xd, wi, wo = x.to(bf).to(DEV), w_in.to(bf).to(DEV), w_out.to(bf).to(DEV)
+    y1 = torch.full((n * k, 1024), 7.0, dtype=bf, device=DEV)
+    y2 = y1.clone()
+    for _ in range(3):                                   # repeated launches reuse the schedule words
+        ops.grouped_swiglu(xd, d, wi, wo, y1)
+    _two_launches(xd, d, wi, wo, y2)
+    ops.experts_check()
+    assert torch.equal(y1, y2)
+    for q in ops._QUEUES.values():
+        assert int(q.abs().sum()) == 0
+    if case == "ragged_e16":
+        xr = x.to(bf).float().numpy()
+        ref = O.experts(xr[np.repeat(np.arange(n), k)], topk.numpy().reshape(-1), w_in.to(bf).float().numpy(),
+                        w_out.to(bf).float().numpy(), act_bf16=True, out_bf16=True)
+        err = rel_err(to_np(y1), ref)
+        print(f"rel err vs oracle {err:.3e}")
+        assert err <= TOL_BF16
+    if valid is not None:
+        assert (to_np(y1)[np.repeat(~valid.numpy(), k)] == 7.0).all()
 
 
 @pytest.mark.parametrize("stride", [128, 16])
