@@ -472,7 +472,10 @@ constexpr int NLMAX = 256;
 // after the stage buffers; the tables follow it
 constexpr int STG_ROWS = 8, STG_WAVE = STG_ROWS * 256, STG = 4 * HALF;
 constexpr int TABLES = STG + NW * STG_WAVE;
-constexpr int LDS_BYTES = TABLES + (2 * (NLMAX + 1) + 2 * BM + 4 + NLMAX) * 4;
+// row tile -> expert, one byte each, for launches of at most RT_TAB row
+// tiles (T <= 256k tokens at top-8); larger ones search the prefix table
+constexpr int RT_TAB = 8192;
+constexpr int LDS_BYTES = TABLES + (2 * (NLMAX + 1) + 2 * BM + 4 + NLMAX) * 4 + RT_TAB;
 static_assert(LDS_BYTES <= 160 * 1024, "LDS budget of one workgroup");
 // buffer resource word 3 for raw 32-bit buffer access on gfx9-family parts
 constexpr int kBufWord3 = 0x00020000;
@@ -634,6 +637,7 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(MoeParams p) {
   int* const s_rows = s_off + NLMAX + 1;                               // [2][BM] row maps
   int* const s_msg = s_rows + 2 * BM;                                  // [4] answers of thread 0's atomics
   int* const s_slot = s_msg + 4;                                       // [NLMAX] weight slot of expert j
+  unsigned char* const s_rt_e = reinterpret_cast<unsigned char*>(s_slot + NLMAX);   // [RT_TAB] expert of row tile R
 
   const int tid = threadIdx.x;
   // wave index as a scalar: keeps per-wave choices (A or weight rows, buffer
@@ -651,6 +655,11 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(MoeParams p) {
   if (tid < 64) scan_units<BM>(s_off, s_prefix, nl, 1);
   __syncthreads();
   const int RT = __builtin_amdgcn_readfirstlane(s_prefix[nl]);
+  const bool rt_tab = RT <= RT_TAB;
+  if (rt_tab)
+    for (int j = tid; j < nl; j += NT)
+      for (int r = s_prefix[j]; r < s_prefix[j + 1]; ++r) s_rt_e[r] = static_cast<unsigned char>(j);
+  __syncthreads();
 
   // ---- queues ---------------------------------------------------------------------
   // Queue qq holds row tiles [lo(qq), lo(qq + 1)); a workgroup starts on its
@@ -682,10 +691,15 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(MoeParams p) {
     R = pos / w;
     c = pos - R * w;
     R += r_lo;
-    int lo = 0, hi = nl - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (s_prefix[mid] <= R) lo = mid; else hi = mid - 1;
+    int lo = 0;
+    if (rt_tab) {
+      lo = s_rt_e[R];
+    } else {
+      int hi = nl - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (s_prefix[mid] <= R) lo = mid; else hi = mid - 1;
+      }
     }
     Tile t;                                        // uniform: keep it in SGPRs
     t.g1 = __builtin_amdgcn_readfirstlane(g1);
@@ -988,10 +1002,10 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(MoeParams p) {
   };
 
   // ---- persistent tile loop ---------------------------------------------------------
-  // Rounds: a workgroup takes two items from a queue (its own first; once
-  // that is drained, the next queue with items left) and runs the pipelined
-  // tile loop over that queue's items, requesting item i + 2 after step 0 of
-  // item i and reading the answer at its end, until the queue runs dry.
+  // Rounds: a workgroup takes one or two items from a queue (its own first;
+  // once that is drained, the next queue with items left) and runs the
+  // pipelined tile loop over that queue's items, claiming the next ones as
+  // it goes (see the claims below), until the queue runs dry.
   std::integral_constant<int, 0> S0;
   std::integral_constant<int, 1> S1;
   std::integral_constant<bool, false> NO;
@@ -1013,8 +1027,12 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(MoeParams p) {
         const int n = q_items(qq);
         a = atomic_add_1(sched + sched::kQueue + qq, 1);
         if (a < n) {
-          b = atomic_add_1(sched + sched::kQueue + qq, 1);
-          if (b >= n) atomic_or_1(sched + sched::kDrained, 1 << qq);
+          // a second item only while this one is a GEMM-1 tile (see the claims below)
+          const bool g2 = MODE == kModeDown || (BOTH && a >= (q_lo(qq + 1) - q_lo(qq)) * n1);
+          if (!g2) {
+            b = atomic_add_1(sched + sched::kQueue + qq, 1);
+            if (b >= n) atomic_or_1(sched + sched::kDrained, 1 << qq);
+          }
           break;
         }
         atomic_or_1(sched + sched::kDrained, 1 << qq);
@@ -1051,11 +1069,22 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(MoeParams p) {
     // Invariant at a tile's start: its stages 0 and 1 are in buffers 0 and 1
     // (landed, published).  Steps are unrolled by four (two stages), so every
     // buffer index is an immediate.
+    bool open = true;                              // no claim on queue cq has come back empty yet
     for (int it = 0;; ++it) {
       const bool act = wm < cur.act_wm;
       const int KT = (cur.g1 ? p.H : p.I) / KS;     // MFMA steps of this tile
+      // Claims, at step KT-8 (step 0 in tiles too short for that): while the
+      // next tile is a GEMM-1 tile, the one after it (a GEMM-1 tile's row map
+      // must be in LDS before the tile in front of it prefetches its first
+      // stages); with no next tile, the next one itself, decoded at step
+      // KT-4 (a GEMM-2 tile needs its row map only in its epilogue).  A
+      // workgroup thus holds at most one unstarted GEMM-2 tile when the queues
+      // run dry.
+      const bool early = KT - 8 < 4;
+      const bool ahead2 = open && has_next && nxt.g1;
+      const bool ahead1 = open && !has_next;
       // a GEMM-2 tile next: poll its row tile's counter at steps KT-8 .. KT-6
-      // (at step 0 for tiles too short for that), read it at step KT-4
+      // (at step 0 for short tiles), read it at step KT-4
       const bool poll = BOTH && has_next && !nxt.g1;
       if (act) first_frags();
       step(S0, YES, NO, YES, sc, 0, 0, 0, act);          // step 0 (stage 0)
@@ -1067,14 +1096,9 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(MoeParams p) {
       // ended step 0: the previous GEMM-1 tile's act rows are complete
       if (BOTH && tid == 0 && sig_r >= 0) atomic_add_1(sched + sched::kRowDone + sig_r, 1);
       sig_r = -1;
-      // item it + 2 is claimed at step KT-8 too (at step 0 in short tiles):
-      // as late as its answer can still reach every wave (through LDS and the
-      // barrier of step KT-2) by the end of this tile, so that a workgroup
-      // holds as few unstarted items as it can when the queues run dry
-      const bool early = KT - 8 < 4;
-      int got = 0, dep = 0;
+      int got = INT_MAX, dep = 0;
       if (tid == 0 && early) {
-        if (has_next) got = atomic_add_1(q_ctr, 1);
+        if (ahead2 || ahead1) got = atomic_add_1(q_ctr, 1);
         if (poll) dep = atomic_read(sched + sched::kRowDone + nxt.R);
       }
       step(S1, NO, YES, YES, sc, 2, 0, 1, act);          // step 1: DMA stage 2 -> buffer 0
@@ -1088,10 +1112,16 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(MoeParams p) {
       for (int k4 = 4; k4 < KT - 4; k4 += 4) {
         const bool late = k4 == KT - 8;
         if (tid == 0 && late) {
-          if (has_next) got = atomic_add_1(q_ctr, 1);
+          if (ahead2 || ahead1) got = atomic_add_1(q_ctr, 1);
           if (poll) dep = atomic_read(sched + sched::kRowDone + nxt.R);
         }
         step(S0, NO, NO, YES, sc, 0, 0, 0, act);
+        // the claim came back before the barrier of step KT-8: a GEMM-2 tile
+        // claimed for next polls its row tile (the row tile is arithmetic)
+        if (BOTH && tid == 0 && late && ahead1) {
+          const int nr = q_lo(cq + 1) - q_lo(cq);
+          if (got < n_items && got >= nr * n1) dep = atomic_read(sched + sched::kRowDone + q_lo(cq) + (got - nr * n1) / n2);
+        }
         step(S1, NO, YES, YES, sc, k4 / 2 + 2, 0, 1, act);
         step(S0, NO, NO, YES, sc, 0, 0, 1, act);
         if (tid == 0 && late) {
@@ -1101,11 +1131,27 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(MoeParams p) {
         step(S1, NO, YES, YES, sc, k4 / 2 + 3, 1, 0, act);
       }
       // last two stages: their odd steps DMA the next tile's stages 0 and 1.
-      // Without a next tile, or with a GEMM-2 tile whose rows are not ready,
-      // they re-read this tile's (in bounds, never consumed) so the code has
-      // no branch here.
+      // Without a next tile, or with one whose first stages cannot stream in
+      // yet (a GEMM-2 tile whose rows are not ready, a GEMM-1 tile claimed
+      // without its row map), they re-read this tile's (in bounds, never
+      // consumed) so the code has no branch here.
       step(S0, NO, NO, YES, sc, 0, 0, 0, act);           // step KT-4
-      const bool ready = has_next && (!poll || __builtin_amdgcn_readfirstlane(s_msg[2]) >= n1);
+      bool ready;
+      if (ahead1) {
+        const int g = __builtin_amdgcn_readfirstlane(s_msg[0]);
+        ready = false;
+        if (g < n_items) {
+          nxt = decode(g, cq);
+          has_next = true;
+          ready = !nxt.g1 && (!BOTH || (!early && __builtin_amdgcn_readfirstlane(s_msg[2]) >= n1));
+          if (ready) rowmap_dma(nxt, (it + 1) & 1);     // read by its epilogue, many barriers on
+        } else {
+          open = false;
+          if (tid == 0) atomic_or_1(sched + sched::kDrained, 1 << cq);
+        }
+      } else {
+        ready = has_next && (!poll || __builtin_amdgcn_readfirstlane(s_msg[2]) >= n1);
+      }
       sc = ready ? setup(nxt, (it + 1) & 1) : setup(cur, it & 1);
       step(S1, NO, YES, YES, sc, 0, 0, 1, act);          // step KT-3: next stage 0 -> buffer 0
       step(S0, NO, NO, YES, sc, 0, 0, 1, act);           // step KT-2
@@ -1119,20 +1165,30 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(MoeParams p) {
         break;
       }
       cur = nxt;
-      const int g = __builtin_amdgcn_readfirstlane(s_msg[0]);
-      has_next = g < n_items;
-      if (has_next) nxt = decode(g, cq);
-      else if (tid == 0) atomic_or_1(sched + sched::kDrained, 1 << cq);
+      has_next = false;
+      if (ahead2) {
+        const int g = __builtin_amdgcn_readfirstlane(s_msg[0]);
+        has_next = g < n_items;
+        if (has_next) {
+          nxt = decode(g, cq);
+        } else {
+          open = false;
+          if (tid == 0) atomic_or_1(sched + sched::kDrained, 1 << cq);
+        }
+      }
       if (!ready) {
-        // the rows of `cur` (a GEMM-2 tile) were not ready: count the tile
-        // just finished, wait between tiles, then load cur's first stages
+        // cur's first stages did not stream in: count the tile just
+        // finished, wait between tiles for cur's rows if it is a GEMM-2
+        // tile, then load its row map and first stages
         __builtin_amdgcn_s_waitcnt(kVmcnt0);
         __syncthreads();
         if (tid == 0) {
           if (BOTH && sig_r >= 0) atomic_add_1(sched + sched::kRowDone + sig_r, 1);
-          if (BOTH) wait_rows(cur.R);
+          if (BOTH && !cur.g1) wait_rows(cur.R);
         }
         sig_r = -1;
+        rowmap_dma(cur, (it + 1) & 1);
+        __builtin_amdgcn_s_waitcnt(kVmcnt0);
         __syncthreads();
         sc = setup(cur, (it + 1) & 1);
 #pragma unroll
