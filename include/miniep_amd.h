@@ -94,7 +94,7 @@ int mep_topk_softmax(const float* logits, int64_t n_tokens, int32_t n_experts,
  * world = 1 with table = 0, g2l = identity is LocalMoEBackend.
  *
  *   topk_idx    (N, k) int64            valid_mask (N,) uint8 or NULL (= all valid)
- *   table       (E, rmax) int32  table[e, j] = rank of e's j-th replica (ep.py:35-45)
+ *   table       (E, rmax) int32  table[e, j] = rank of e's j-th replica (ep.py:35-45), rmax <= 32
  *   n_rep       (E,) int32       >= 1
  *   has_replicas  0 iff every n_rep[e] == 1; then dest = table[e, 0] and rr
  *                 is neither read nor written (ep.py:84-85)

@@ -43,6 +43,7 @@ constexpr int kThreads = 512;
 constexpr int kChunk = 512;           // entries per block: one round of the block
 constexpr int kMaxSeg = 16;
 constexpr int kMaxExperts = 256;
+constexpr int kMaxReplicas = 32;      // replica slots per expert (a 32-bit mask of this rank's slots)
 // above this many blocks the histograms are scanned once by prefix_kernel
 // instead of being summed again by every scatter block (nb^2 * E reads)
 constexpr int kScanBlocks = 512;
@@ -102,16 +103,23 @@ __device__ __forceinline__ int reps(const DispatchParams& p, int e) {
   return r < 1 ? 1 : (r > p.rmax ? p.rmax : r);
 }
 
-// #{w' in [0, w) : (rr + w') mod R == j}, summed over the slots j this rank holds.
+// rr mod R with the sign of R (torch's % on int64 tensors, ep.py:94), in [0, R)
+__device__ __forceinline__ int floor_mod(int64_t rr, int R) {
+  const int m = static_cast<int>(rr % R);
+  return m < 0 ? m + R : m;
+}
 
-__device__ __forceinline__ int64_t kept_before(const DispatchParams& p, int e, int64_t w, int64_t rr) {
-  const int R = reps(p, e);
-  int64_t n = 0;
-  const int64_t rmod = rr % R;
+// #{w' in [0, w) : (rr + w') mod R == j}, summed over the slots j this rank
+// holds (bit j of `mine`; R replicas; rrmod = rr mod R).  32-bit: w counts
+// the entries of one expert in one segment (< 2^31), and rr enters only
+// through rrmod, so no 64-bit division runs per entry.
+__device__ __forceinline__ int kept_before(uint32_t mine, int R, uint32_t w, int rrmod) {
+  int n = 0;
   for (int j = 0; j < R; ++j) {
-    if (p.table[e * p.rmax + j] != p.my_rank) continue;
-    const int64_t c = ((j - rmod) % R + R) % R;
-    if (w > c) n += (w - c - 1) / R + 1;
+    if (!((mine >> j) & 1u)) continue;
+    int c = j - rrmod;
+    if (c < 0) c += R;
+    if (w > static_cast<uint32_t>(c)) n += static_cast<int>((w - c - 1) / static_cast<uint32_t>(R)) + 1;
   }
   return n;
 }
@@ -203,8 +211,17 @@ __global__ __launch_bounds__(kScanThreads) void prefix_kernel(DispatchParams p) 
   }
 }
 
+// LDS copy of the replica table in scatter_kernel when it has at most this many entries
+constexpr int kTabLds = 2048;
+
 __global__ __launch_bounds__(kThreads) void scatter_kernel(DispatchParams p) {
   __shared__ int segtot[kMaxSeg][kMaxExperts];   // entries of expert e in segment s
+  // per-expert tables, copied once per block (every entry looks them up):
+  __shared__ int s_tab[kTabLds];                 // table (E x rmax) when it fits
+  __shared__ int s_R[kMaxExperts];               // replica count (clamped to [1, rmax])
+  __shared__ uint32_t s_mine[kMaxExperts];       // bit j: table[e][j] == my_rank
+  __shared__ int s_g2l[kMaxExperts];
+  __shared__ int s_rrmod[kMaxSeg * kMaxExperts]; // rr[segment][e] mod R
   __shared__ int pre[kMaxExperts];                // ... in earlier blocks of my segment
   __shared__ int keptbase[kMaxExperts];           // kept entries of e in earlier segments
   __shared__ int loff[kMaxExperts];               // first row of e's local expert
@@ -230,6 +247,20 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(DispatchParams p) {
     else dropped = true;
   }
 
+  // the per-expert tables: their loads go out with the entry's, before the first barrier
+  const bool tab_lds = E * p.rmax <= kTabLds;
+  if (tab_lds)
+    for (int i = tid; i < E * p.rmax; i += kThreads) s_tab[i] = p.table[i];
+  for (int e = tid; e < E; e += kThreads) {
+    const int R = reps(p, e);
+    uint32_t mine = 0;
+    for (int j = 0; j < R && j < 32; ++j) mine |= (p.table[e * p.rmax + j] == p.my_rank ? 1u : 0u) << j;
+    s_R[e] = R;
+    s_mine[e] = mine;
+    s_g2l[e] = p.g2l[e];
+  }
+  if (p.has_rep)
+    for (int i = tid; i < p.n_seg * E; i += kThreads) s_rrmod[i] = floor_mod(p.rr_snap[i], reps(p, i % E));
   for (int i = tid; i < p.n_seg * kMaxExperts; i += kThreads) segtot[i / kMaxExperts][i % kMaxExperts] = 0;
   for (int e = tid; e < E; e += kThreads) { pre[e] = 0; lcount[e] = 0; }
   for (int i = tid; i < (kThreads / 64) * (kMaxExperts + 1); i += kThreads)
@@ -277,20 +308,22 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(DispatchParams p) {
   // 2. kept entries per (segment, expert) -> local counts and my segment base
   for (int e = tid; e < E; e += kThreads) {
     int64_t total = 0, base = 0;
+    const uint32_t mine = s_mine[e];
+    const int R = s_R[e];
     for (int sg = 0; sg < p.n_seg; ++sg) {
       int64_t kept;
-      if (p.has_rep) kept = kept_before(p, e, segtot[sg][e], p.rr_snap[sg * E + e]);
-      else kept = (p.table[e * p.rmax] == p.my_rank) ? segtot[sg][e] : 0;
+      if (p.has_rep) kept = kept_before(mine, R, static_cast<uint32_t>(segtot[sg][e]), s_rrmod[sg * E + e]);
+      else kept = (mine & 1u) ? segtot[sg][e] : 0;
       if (sg < s) base += kept;
       total += kept;
     }
     keptbase[e] = static_cast<int>(base);
-    const int j = p.g2l[e];
+    const int j = s_g2l[e];
     if (j >= 0 && j < p.n_local) lcount[j] = static_cast<int>(total);
   }
   __syncthreads();
   for (int e = tid; e < E; e += kThreads) {
-    const int j = p.g2l[e];
+    const int j = s_g2l[e];
     int off = 0;
     if (j >= 0 && j < p.n_local)
       for (int jj = 0; jj < j; ++jj) off += lcount[jj];
@@ -335,17 +368,17 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(DispatchParams p) {
     int w = pre[key] + rank_w;
     for (int ww = 0; ww < wave; ++ww) w += wcnt[ww][key];
     const int e = key;
-    const int64_t rr0 = p.has_rep ? p.rr_snap[s * E + e] : 0;
-    const int R = reps(p, e);
-    // floor modulo, as torch's % on int64 tensors (ep.py:94)
-    const int slot = p.has_rep ? static_cast<int>(((rr0 + w) % R + R) % R) : 0;
-    const int d = p.table[e * p.rmax + slot];
+    const int rrmod = p.has_rep ? s_rrmod[s * E + e] : 0;
+    const int R = s_R[e];
+    // (rr + w) mod R, floor modulo as torch's % on int64 tensors (ep.py:94)
+    const int slot = p.has_rep ? static_cast<int>((static_cast<uint32_t>(rrmod) + static_cast<uint32_t>(w)) % static_cast<uint32_t>(R)) : 0;
+    const int d = tab_lds ? s_tab[e * p.rmax + slot] : p.table[e * p.rmax + slot];
     if (p.dest != nullptr) p.dest[f] = d;
     int row = -1;
     if (d == p.my_rank) {
-      const int j = p.g2l[e];
+      const int j = s_g2l[e];
       if (j >= 0 && j < p.n_local) {
-        const int64_t kb = p.has_rep ? kept_before(p, e, w, rr0) : w;
+        const int kb = p.has_rep ? kept_before(s_mine[e], R, static_cast<uint32_t>(w), rrmod) : w;
         row = loff[e] + keptbase[e] + static_cast<int>(kb);
         p.perm[row] = static_cast<int32_t>(f);
       } else {
@@ -460,6 +493,7 @@ int dispatch_impl(const char* fn, const int64_t* topk_idx, const uint8_t* valid_
   MEP_REQUIRE(n_tokens * top_k < (int64_t(1) << 31), MEP_ERR_UNSUPPORTED,
               "%s: n_tokens * top_k must be < 2^31", fn);
   MEP_REQUIRE(rmax >= 1, MEP_ERR_INVALID_ARG, "%s: rmax %d < 1", fn, rmax);
+  MEP_REQUIRE(rmax <= kMaxReplicas, MEP_ERR_UNSUPPORTED, "%s: rmax %d > %d replicas", fn, rmax, kMaxReplicas);
   MEP_REQUIRE(n_local >= 0 && n_local <= n_experts, MEP_ERR_INVALID_ARG,
               "%s: n_local %d outside [0, %d]", fn, n_local, n_experts);
   MEP_REQUIRE(n_segments >= 1 && n_segments <= kMaxSeg && seg_tokens != nullptr,
