@@ -9,8 +9,8 @@ intermediate 512), T = 16384 tokens whose routing is Zipf(1.2)-skewed
 weights N(0, 0.02).  One step = the whole hot path over the batch, inputs
 already resident in HBM:
 
-    router (GEMV + top-8 + softmax, with the dispatch's per-block expert
-    histograms) -> dispatch scatter (stable rank, permutation) -> grouped
+    router + dispatch, one launch (GEMV + top-8 + softmax, then the stable
+    rank of every entry per expert and the permutation) -> grouped
     experts, one launch: GEMM-1 + SwiGLU (gathered rows) and GEMM-2
     (scattered to (token, slot) cells), each XCD's GEMM-2 tiles starting
     once their rows' GEMM-1 tiles are done -> combine (gate-weighted
@@ -164,7 +164,7 @@ def decode_detail(dev, calls: int = 200) -> dict:
     """The decode-shaped layer (32 tokens, bf16, unbiased router: near-uniform
     load, most experts with 0-16 entries), HBM-bound on streaming the expert
     weights of the experts it touches.  One call = route + dispatch, GEMM-1,
-    GEMM-2, combine (HipMoEBackend.route_and_call, 5 launches).  At this size
+    GEMM-2, combine (HipMoEBackend.route_and_call, 4 launches).  At this size
     the host's enqueue time is close to the GPU time, so the call is also
     captured in a HIP graph and replayed (a decode loop could replay it the
     same way); every replay is checked against the eager output.  HIP events
@@ -223,7 +223,7 @@ def decode_detail(dev, calls: int = 200) -> dict:
             "us_per_call": 1e3 * best, "us_per_call_eager": 1e3 * eager_ms, "us_per_call_graph": 1e3 * ms,
             "replays_equal_eager": replays_equal, "bytes": nbytes, "GB/s": nbytes / (best / 1e3) / 1e9,
             "frac_hbm": nbytes / (best / 1e3) / PEAK_HBM_BYTES, "floor_us": 1e6 * nbytes / PEAK_HBM_BYTES,
-            "measures": f"route_and_call (5 launches), {calls} calls back to back, HIP events, launched from Python "
+            "measures": f"route_and_call (4 launches), {calls} calls back to back, HIP events, launched from Python "
                         "(eager) and replayed from a HIP graph (graph); us_per_call is the faster of the two"}
 
 
@@ -372,9 +372,9 @@ def main(argv=None) -> int:
     stages = ["route_dispatch", "gemm1_swiglu", "gemm2_scatter", "combine"]
 
     def step(g=None):
-        """One pass of the hot path (4 calls: router with the dispatch
-        histograms + dispatch scatter, the grouped experts in one launch,
-        combine); `g` = 2 events around the grouped-experts launch."""
+        """One pass of the hot path (3 launches: router + dispatch, the
+        grouped experts, combine); `g` = 2 events around the grouped-experts
+        launch."""
         idx, gate, disp = ops.route_dispatch(x, w_r, K, None, check=False)
         if g is not None:
             g[0].record()
@@ -448,9 +448,9 @@ def main(argv=None) -> int:
     exp_ms = sum(e[0].elapsed_time(e[1]) for e in g_events) / args.steps
     flops_g1 = 2.0 * M * H * 2 * I
     flops_g2 = 2.0 * M * I * H
-    # router: x and W_r in, indices (int64) and gates (bf16) out; dispatch
-    # scatter: the indices read back, perm and row_of_entry (int32) out
-    route_bytes = T * H * 2 + E * H * 2 + T * K * (8 + 2) + T * K * 8 + 2 * T * K * 4
+    # router + dispatch: x and W_r in; indices (int64), gates (bf16), perm
+    # and row_of_entry (int32) out
+    route_bytes = T * H * 2 + E * H * 2 + T * K * (8 + 2) + 2 * T * K * 4
     combine_bytes = M * H * 2 + T * K * (2 + 4) + T * H * 2
     g1_s = stage_ms["gemm1_swiglu"] / 1e3
     g2_s = stage_ms["gemm2_scatter"] / 1e3

@@ -137,6 +137,7 @@ int mep_dispatch_check(const void* workspace, void* stream);
 #define MEP_DISPATCH_STATUS_RANGE 1u          /* an expert id outside [0, n_experts) was dropped      */
 #define MEP_DISPATCH_STATUS_NOT_RESIDENT 2u   /* an entry for a non-resident expert was dropped      */
 #define MEP_DISPATCH_STATUS_REPLICAS 4u       /* some n_rep[e] lies outside [1, rmax]                 */
+#define MEP_DISPATCH_STATUS_BARRIER 8u        /* mep_route_dispatch: a workgroup gave up waiting     */
 
 /* mep_dispatch without a workspace argument: it allocates nothing and takes
  * no workspace.  No counterpart in the reference; it is for callers that
@@ -172,6 +173,15 @@ int mep_dispatch_noalloc(const int64_t* topk_idx, const uint8_t* valid_mask, int
  * those of the two calls, bit for bit; route_counts (E,) int64 or NULL:
  * += per-expert valid-entry counts.  Supported: top_k = 8, E in {16, 32, 64},
  * H % 256 == 0; other shapes use the two calls.
+ * GraniteMoE's shape (bf16, E = 32, H in {1024, 2048, 4096}) runs as ONE
+ * launch when its ceil(N / 64) workgroups fit on the device at once (e.g.
+ * N <= 32768 on 256 CUs at hidden 1024): each workgroup publishes its
+ * per-expert counts, reads everyone's and places its own entries.  The
+ * published counts carry a per-call tag kept in the workspace, so the
+ * workspace must be zero-filled once when it is allocated and then reused
+ * as is; calls that overlap in time (different streams) need different
+ * workspaces.  mep_dispatch_check reports MEP_ERR_HIP if a workgroup gave up
+ * waiting for the others (they were not all resident).
  * ---------------------------------------------------------------------- */
 size_t mep_route_dispatch_workspace_size(int64_t n_tokens, int32_t n_experts);
 

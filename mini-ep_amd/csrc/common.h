@@ -69,6 +69,22 @@ hipError_t launch_router_with_hist(const void* x, const void* w, int64_t n, int 
                                    uint32_t* flags, int32_t* tables, const uint8_t* valid, int n_blocks,
                                    hipStream_t stream);
 
+// The fused router + dispatch (one launch) of the all-local backend for
+// bf16, E = 32, top-8, hidden 1024 / 2048 / 4096: outputs as
+// mep_route_dispatch.  `rows` holds n_blocks x E tagged histogram words and
+// the workspace header's word 32 the epoch; both must be zero before the
+// first call on a workspace.  Returns hipErrorNotSupported, with nothing
+// enqueued, when the shape differs or when the n_blocks workgroups do not
+// all fit on the device at once.
+hipError_t launch_route_dispatch_fused(const void* x, const void* w, int64_t n, int hidden, int E, int k, int dtype,
+                                       int64_t* idx, void* gate, float* logits, int32_t* counts, int32_t* offsets,
+                                       int32_t* perm, int32_t* row_of_entry, int64_t* route_counts, uint64_t* rows,
+                                       uint32_t* header, uint32_t* flags, const uint8_t* valid, int n_blocks,
+                                       hipStream_t stream);
+// dispatch status bit of the fused route + dispatch: a workgroup gave up
+// waiting for another's histogram row
+constexpr uint32_t kFlagBarrier = 8u;
+
 inline int dtype_bytes(int dtype) {
   return dtype == MEP_DTYPE_F32 ? 4 : (dtype == MEP_DTYPE_BF16 ? 2 : 0);
 }

@@ -612,6 +612,10 @@ __global__ void empty_route_kernel(int n_local, int32_t* counts, int32_t* offset
 }
 
 size_t route_tables_offset(const WsLayout& l) { return l.total; }
+// tagged histogram rows of the fused route + dispatch, after the tables
+size_t route_rows_offset(const WsLayout& l, int E) {
+  return route_tables_offset(l) + align_up(sizeof(int32_t) * 3 * E, 256);
+}
 
 WsLayout route_layout(int64_t n_tokens, int32_t n_experts, int* nb_out) {
   const int nb = static_cast<int>((n_tokens * 8 + kChunk - 1) / kChunk);
@@ -626,7 +630,7 @@ extern "C" size_t mep_route_dispatch_workspace_size(int64_t n_tokens, int32_t n_
   if (n_tokens < 0 || n_experts <= 0 || n_experts > kMaxExperts) return 0;
   int nb = 0;
   const WsLayout l = route_layout(n_tokens, n_experts, &nb);
-  return route_tables_offset(l) + align_up(sizeof(int32_t) * 3 * n_experts, 256);
+  return route_rows_offset(l, n_experts) + sizeof(uint64_t) * static_cast<size_t>(nb > 0 ? nb : 1) * n_experts;
 }
 
 extern "C" int mep_route_dispatch(const void* x, const void* w_router, const uint8_t* valid_mask, int64_t n_tokens,
@@ -663,8 +667,17 @@ extern "C" int mep_route_dispatch(const void* x, const void* w_router, const uin
     MEP_CHECK_LAUNCH("mep_route_dispatch(empty)");
     return MEP_OK;
   }
+  // one launch when the shape has the fused kernel and its workgroups fit on
+  // the device at once
+  hipError_t e = launch_route_dispatch_fused(x, w_router, n_tokens, hidden, n_experts, top_k, dtype, topk_idx,
+                                             topk_gate, logits, counts, offsets, perm, row_of_entry, route_counts,
+                                             reinterpret_cast<uint64_t*>(ws + route_rows_offset(l, n_experts)),
+                                             reinterpret_cast<uint32_t*>(ws + l.header),
+                                             reinterpret_cast<uint32_t*>(ws + l.flags), valid_mask, nb, st);
+  if (e == hipSuccess) return MEP_OK;
+  MEP_REQUIRE(e == hipErrorNotSupported, MEP_ERR_HIP, "%s: fused launch failed: %s", fn, hipGetErrorString(e));
   int32_t* tables = reinterpret_cast<int32_t*>(ws + route_tables_offset(l));
-  hipError_t e = launch_router_with_hist(x, w_router, n_tokens, hidden, n_experts, top_k, dtype, topk_idx,
+  e = launch_router_with_hist(x, w_router, n_tokens, hidden, n_experts, top_k, dtype, topk_idx,
                                          topk_gate, logits, reinterpret_cast<int32_t*>(ws + l.bc),
                                          reinterpret_cast<uint32_t*>(ws + l.header),
                                          reinterpret_cast<uint32_t*>(ws + l.flags), tables, valid_mask, nb, st);
@@ -720,8 +733,11 @@ extern "C" int mep_dispatch_check(const void* workspace, void* stream) {
     for (uint32_t j = 0; j < n; ++j) acc |= buf[j];
   }
   static_assert(kFlagRange == MEP_DISPATCH_STATUS_RANGE && kFlagResident == MEP_DISPATCH_STATUS_NOT_RESIDENT &&
-                    kFlagReplicas == MEP_DISPATCH_STATUS_REPLICAS,
+                    kFlagReplicas == MEP_DISPATCH_STATUS_REPLICAS && kFlagBarrier == MEP_DISPATCH_STATUS_BARRIER,
                 "status bits of the header");
+  MEP_REQUIRE(!(acc & kFlagBarrier), MEP_ERR_HIP,
+              "mep_route_dispatch: a workgroup gave up waiting for the others' histogram rows (workgroups not "
+              "resident together); results invalid");
   MEP_REQUIRE(!(acc & kFlagReplicas), MEP_ERR_INVALID_ARG,
               "mep_dispatch: n_rep[e] outside [1, rmax] for some expert (every expert needs an owner)");
   MEP_REQUIRE(!(acc & kFlagRange), MEP_ERR_EXPERT_RANGE,

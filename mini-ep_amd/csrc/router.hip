@@ -22,6 +22,8 @@
 // the entries per expert of its 64 tokens.
 #include "common.h"
 
+#include <atomic>
+
 namespace mep {
 namespace {
 
@@ -207,7 +209,8 @@ struct RouterHist {
 template <int GATE_DT, int EC, int KC>
 __device__ void select_topk_wave(const float* lg, int ld, int64_t t0, int64_t n_tokens, float* sel_val,
                                  int* sel_idx, int64_t* topk_idx, typename Elem<GATE_DT>::T* gate,
-                                 uint64_t* keys, int kld, const RouterHist& hist, int* s_cnt) {
+                                 uint64_t* keys, int kld, const RouterHist& hist, int* s_cnt,
+                                 int* sel_out) {
   static_assert(EC % 4 == 0 && KC % 4 == 0 && KC <= EC && kRowsPerWave * 4 == 64, "lane layout");
   constexpr int EG = EC / 4, SG = KC / 4;
   const int lane = lane_id();
@@ -285,6 +288,13 @@ __device__ void select_topk_wave(const float* lg, int ld, int64_t t0, int64_t n_
       my_gate[h] = ex[g * SG + h] / sum;
     }
   }
+  if (sel_out != nullptr) {
+    // the experts of this lane's slots for the fused dispatch: -1 for tokens
+    // past the end or masked out
+    const bool counted = t0 + t < n_tokens && (hist.valid == nullptr || hist.valid[t0 + t] != 0);
+#pragma unroll
+    for (int h = 0; h < SG; ++h) sel_out[h] = counted ? my_idx[h] : -1;
+  }
   if (t0 + t < n_tokens) {
 #pragma unroll
     for (int h = 0; h < SG; ++h) {
@@ -308,7 +318,7 @@ __device__ __forceinline__ void router_tail(const f32x4* acc, float (*lgw)[E + 1
                                             int* sel_idxw, float* rsumw, int* s_cnt, int64_t t0, int64_t n_tokens,
                                             int k, int64_t* __restrict__ topk_idx,
                                             typename Elem<DT>::T* __restrict__ gate, float* __restrict__ logits,
-                                            const RouterHist& hist) {
+                                            const RouterHist& hist, int* sel_out = nullptr) {
   constexpr int NF = E / 16;
   const int tid = threadIdx.x, lane = lane_id();
   const int r = lane & 15, g = lane >> 4;
@@ -332,7 +342,7 @@ __device__ __forceinline__ void router_tail(const f32x4* acc, float (*lgw)[E + 1
   }
   if constexpr (kWaveSelect) {
     select_topk_wave<DT, E, KC>(&lgw[0][0], E + 1, t0, n_tokens, sel_valw, sel_idxw, topk_idx, gate, keysw, E + 2,
-                                hist, s_cnt);
+                                hist, s_cnt, sel_out);
     if (hist.bc != nullptr) {
       // the workgroup's histogram is the dispatch's histogram of block b
       __syncthreads();
@@ -479,34 +489,22 @@ __global__ __launch_bounds__(kWaves * 64) void router_kernel(const typename Elem
 // runs the MFMAs of each 256-wide K block as that block of x arrives, with
 // the block's 16 weight fragments read from LDS before its 16 MFMAs (read
 // and multiply interleaved one by one, the LDS latency is paid 64 times).
+// One wave's 16 x 32 logit tile of the GraniteMoE router shape (bf16, 32
+// experts, hidden 1024 * NSEG); `ws` is the workgroup's LDS copy of one W_r
+// segment.  Called by every thread of the workgroup (it contains barriers).
 template <int NSEG>
-__global__ __launch_bounds__(kWaves * 64) void router32_kernel(const uint16_t* __restrict__ x,
-                                                               const uint16_t* __restrict__ w, int64_t n_tokens,
-                                                               int64_t* __restrict__ topk_idx,
-                                                               uint16_t* __restrict__ gate,
-                                                               float* __restrict__ logits, RouterHist hist) {
-  constexpr int E = 32, NF = 2, KC = 8, H = 1024 * NSEG;
+__device__ __forceinline__ void router32_logits(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+                                                int64_t n_tokens, int64_t t0, unsigned char* ws, f32x4 (&acc)[2]) {
+  constexpr int E = 32, NF = 2, H = 1024 * NSEG;
   constexpr int kRowStride = 1024 * 2 + 16;        // bytes of one W_r row segment in LDS (16 B pad: conflict-free)
-  __shared__ __attribute__((aligned(16))) unsigned char ws[E * kRowStride];
-  __shared__ float lg[kWaves][kRowsPerWave][E + 1];
-  __shared__ __attribute__((aligned(16))) uint64_t keys[kWaves][kRowsPerWave * (E + 2)];
-  __shared__ __attribute__((aligned(16))) float sel_val[kWaves][kRowsPerWave * KC];
-  __shared__ int sel_idx[kWaves][kRowsPerWave * KC];
-  __shared__ float rsum[kWaves][kRowsPerWave];
-  __shared__ int s_cnt[E];
-
-  const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
+  const int tid = threadIdx.x, lane = lane_id();
   const int r = lane & 15, g = lane >> 4;
-  if (tid < E) s_cnt[tid] = 0;                    // published by the first barrier below
-  const int64_t t0 = (static_cast<int64_t>(blockIdx.x) * kWaves + wave) * kRowsPerWave;
   int64_t tok = t0 + r;
   if (tok >= n_tokens) tok = n_tokens - 1;        // in-bounds read, result discarded
   const uint16_t* xrow = x + tok * H + g * 8;
   // W_r chunk i of this thread: row (tid >> 7) + 2 i, 16 bytes at column (tid & 127) * 8
   const uint16_t* wrow = w + static_cast<int64_t>(tid >> 7) * H + (tid & 127) * 8;
   const int wlds = (tid >> 7) * kRowStride + (tid & 127) * 16;
-
-  f32x4 acc[NF];
 #pragma unroll
   for (int nf = 0; nf < NF; ++nf) acc[nf] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -542,8 +540,253 @@ __global__ __launch_bounds__(kWaves * 64) void router32_kernel(const uint16_t* _
       __builtin_amdgcn_sched_barrier(0);
     }
   }
-  router_tail<MEP_DTYPE_BF16, E, KC>(acc, lg[wave], keys[wave], sel_val[wave], sel_idx[wave], rsum[wave], s_cnt, t0,
-                                      n_tokens, KC, topk_idx, gate, logits, hist);
+}
+
+constexpr int kRowStride32 = 1024 * 2 + 16;
+
+template <int NSEG>
+__global__ __launch_bounds__(kWaves * 64) void router32_kernel(const uint16_t* __restrict__ x,
+                                                               const uint16_t* __restrict__ w, int64_t n_tokens,
+                                                               int64_t* __restrict__ topk_idx,
+                                                               uint16_t* __restrict__ gate,
+                                                               float* __restrict__ logits, RouterHist hist) {
+  constexpr int E = 32, KC = 8;
+  __shared__ __attribute__((aligned(16))) unsigned char ws[E * kRowStride32];
+  __shared__ float lg[kWaves][kRowsPerWave][E + 1];
+  __shared__ int s_cnt[E];
+  const int tid = threadIdx.x, wave = tid >> 6;
+  if (tid < E) s_cnt[tid] = 0;                    // published by the first barrier of router32_logits
+  const int64_t t0 = (static_cast<int64_t>(blockIdx.x) * kWaves + wave) * kRowsPerWave;
+  f32x4 acc[2];
+  router32_logits<NSEG>(x, w, n_tokens, t0, ws, acc);
+  // the E = 32, top-8 selection runs in registers: no key / selection scratch
+  router_tail<MEP_DTYPE_BF16, E, KC>(acc, lg[wave], nullptr, nullptr, nullptr, nullptr, s_cnt, t0, n_tokens, KC,
+                                      topk_idx, gate, logits, hist);
+}
+
+// ---------------------------------------------------------------------------
+// Router and dispatch of the all-local backend in one launch (GraniteMoE's
+// shape: bf16, 32 experts, top-8).  Each workgroup routes its 64 tokens as
+// router32_kernel does; its 512 entries are then one dispatch block.  It ranks
+// them by flat entry id per expert inside the block (a token's 8 experts are
+// distinct, so an entry's rank is the number of earlier tokens of the block
+// that chose the same expert: wave ballots over the 5 id bits, then the waves'
+// counts in order) and publishes its histogram row.  From every workgroup's
+// row it takes the expert totals (counts, offsets) and its own prefix over
+// earlier blocks, which place every entry:
+//   row = offsets[e] + #(e in earlier blocks) + #(e earlier in this block),
+// the stable grouping by expert of modeling.py:94-96.  Results equal
+// router32_kernel followed by the dispatch's scatter_kernel bit for bit.
+//
+// Every workgroup must be resident at once (the host launches at most as
+// many as the device holds).  There is no counter and no atomic: each row
+// word is a 64-bit (tag << 32 | count) written and read with device-scope
+// (sc1) accesses, so a word written on one XCD is read fresh on every other,
+// and a workgroup re-reads the words whose tag is not yet this call's.  The
+// tag is 2^31 | (the workspace's epoch word + 1): every workgroup reads the
+// epoch as it starts, and workgroup 0 advances it once it has seen every row
+// of this call (by then every workgroup has read it).  Words of earlier calls
+// carry older tags, and whatever else the library leaves in a workspace
+// (counts, flags, table entries: small non-negative values) has a clear top
+// bit, so the workspace must only be zero-filled once before its first use
+// and can then serve calls of any size.  A wait longer than kRowPolls polls sets
+// kFlagBarrier in the block's status word: every workgroup exits, and
+// mep_dispatch_check reports it.
+constexpr int kEpochWord = 32;                    // header word of the epoch (its own 128-byte line)
+constexpr int kRowPolls = 1 << 20;
+
+struct FusedDispatch {
+  int32_t* counts;          // (E,) rows per expert
+  int32_t* offsets;         // (E + 1,) exclusive prefix of counts
+  int32_t* perm;            // (N k,) perm[row] = flat entry id
+  int32_t* row_of_entry;    // (N k,) row of each entry, -1 for masked tokens
+  int64_t* route_counts;    // (E,) += entries per expert, or NULL
+  uint64_t* rows;           // (n_blocks, E) tagged histogram rows
+  uint32_t* header;         // [0] = n_blocks; [kEpochWord]: the epoch
+  uint32_t* flags;          // (2 n_blocks,) status words: count pass (0), scatter pass
+  const uint8_t* valid;     // (N,) or NULL
+};
+
+__device__ __forceinline__ int load_dev(const int32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t load_dev(const uint32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t load_dev(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_dev(uint64_t* p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_dev(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Lanes whose expert in key array `bits` (the 5 id-bit ballots, `present` =
+// lanes with an expert) equals v.
+__device__ __forceinline__ uint64_t lanes_with(int v, const uint64_t (&bits)[5], uint64_t present) {
+  uint64_t m = present;
+#pragma unroll
+  for (int i = 0; i < 5; ++i) m &= ((v >> i) & 1) ? bits[i] : ~bits[i];
+  return m;
+}
+
+template <int NSEG>
+__global__ __launch_bounds__(kWaves * 64) void route_dispatch32_kernel(const uint16_t* __restrict__ x,
+                                                                       const uint16_t* __restrict__ w,
+                                                                       int64_t n_tokens,
+                                                                       int64_t* __restrict__ topk_idx,
+                                                                       uint16_t* __restrict__ gate,
+                                                                       float* __restrict__ logits, FusedDispatch o) {
+  constexpr int E = 32, KC = 8;
+  constexpr int kParts = kWaves * 64 / E;         // 8 threads per expert sum the histogram rows
+  __shared__ __attribute__((aligned(16))) unsigned char ws[E * kRowStride32];
+  __shared__ float lg[kWaves][kRowsPerWave][E + 1];
+  __shared__ int s_wcnt[kWaves][E];               // entries of expert e in wave w of this block
+  __shared__ int s_part[kParts][2][E];            // per part: entries in earlier blocks / in all blocks
+  __shared__ int s_base[E];                       // first row of expert e's entries of this block
+  __shared__ uint32_t s_flag;
+  const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
+  const int b = blockIdx.x, nb = gridDim.x;
+  if (tid < kWaves * E) s_wcnt[tid / E][tid % E] = 0;   // published by the first barrier of router32_logits
+  if (tid == 0) s_flag = 0u;
+  const int64_t t0 = (static_cast<int64_t>(b) * kWaves + wave) * kRowsPerWave;
+  // this call's tag; the load goes out before the router's loads and has
+  // long landed when the tag is first used
+  const uint32_t epoch = (load_dev(o.header + kEpochWord) + 1u) & 0x7fffffffu;
+  const uint64_t tag = static_cast<uint64_t>(0x80000000u | epoch) << 32;
+  asm volatile("" ::: "memory");
+  f32x4 acc[2];
+  router32_logits<NSEG>(x, w, n_tokens, t0, ws, acc);
+  RouterHist hist{};
+  hist.valid = o.valid;
+  int sel[2];                                     // experts of this lane's two slots, -1: not dispatched
+  router_tail<MEP_DTYPE_BF16, E, KC>(acc, lg[wave], nullptr, nullptr, nullptr, nullptr, nullptr, t0, n_tokens, KC,
+                                      topk_idx, gate, logits, hist, sel);
+
+  // 1. rank of each entry among the wave's entries of its expert (lane order =
+  // token order; the two slots of a lane hold different experts)
+  uint64_t bits0[5], bits1[5];
+#pragma unroll
+  for (int i = 0; i < 5; ++i) {
+    bits0[i] = __ballot((sel[0] >> i) & 1);
+    bits1[i] = __ballot((sel[1] >> i) & 1);
+  }
+  const uint64_t has0 = __ballot(sel[0] >= 0), has1 = __ballot(sel[1] >= 0);
+  const uint64_t before = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  int rank[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int e = sel[h];
+    const uint64_t m = e >= 0 ? (lanes_with(e, bits0, has0) | lanes_with(e, bits1, has1)) : 0ull;
+    rank[h] = __popcll(m & before);
+    if (e >= 0 && rank[h] == 0) s_wcnt[wave][e] = __popcll(m);
+  }
+  __syncthreads();
+
+  // 2. this block's histogram row, then every block's: rows bb = part + 8 u
+  // of this thread's expert column, re-read until each carries this call's
+  // tag (one workgroup: its own counts, nothing to publish)
+  if (nb == 1) {
+    const int e = tid % E, part = tid / E;
+    int c = 0;
+    if (part == 0)
+#pragma unroll
+      for (int ww = 0; ww < kWaves; ++ww) c += s_wcnt[ww][e];
+    s_part[part][0][e] = 0;
+    s_part[part][1][e] = c;
+  } else {
+    if (tid < E) {
+      int c = 0;
+#pragma unroll
+      for (int ww = 0; ww < kWaves; ++ww) c += s_wcnt[ww][tid];
+      store_dev(o.rows + static_cast<int64_t>(b) * E + tid, tag | static_cast<uint32_t>(c));
+    }
+    const int e = tid % E, part = tid / E;
+    int pre = 0, tot = 0;
+    uint32_t bad = 0u;
+    constexpr int kBatch = 32;
+    for (int bb0 = part; bb0 < nb; bb0 += kParts * kBatch) {
+      uint64_t v[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int bb = bb0 + u * kParts;
+        v[u] = bb < nb ? load_dev(o.rows + static_cast<int64_t>(bb) * E + e) : tag;
+      }
+      for (int it = 0;; ++it) {
+        bool stale = false;
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) stale |= (v[u] & ~0xffffffffull) != tag;
+        if (!stale) break;
+        if (it >= kRowPolls) { bad = kFlagBarrier; break; }
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u)
+          if ((v[u] & ~0xffffffffull) != tag) v[u] = load_dev(o.rows + static_cast<int64_t>(bb0 + u * kParts) * E + e);
+      }
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int bb = bb0 + u * kParts;
+        const int c = static_cast<int>(static_cast<uint32_t>(v[u]));
+        tot += c;
+        pre += bb < b ? c : 0;
+      }
+    }
+    s_part[part][0][e] = pre;
+    s_part[part][1][e] = tot;
+    if (bad) s_flag = bad;
+  }
+  __syncthreads();
+  if (tid < E) {
+    int pre = 0, tot = 0;
+#pragma unroll
+    for (int q = 0; q < kParts; ++q) { pre += s_part[q][0][tid]; tot += s_part[q][1][tid]; }
+    int incl = tot;                                // inclusive prefix over experts (lanes 0..31 of wave 0)
+#pragma unroll
+    for (int d = 1; d < E; d <<= 1) {
+      const int v = __shfl_up(incl, d, 64);
+      if (lane >= d) incl += v;
+    }
+    const int off = incl - tot;
+    s_base[tid] = off + pre;
+    if (b == 0) {
+      o.counts[tid] = tot;
+      o.offsets[tid] = off;
+      if (tid == E - 1) o.offsets[E] = incl;
+      if (o.route_counts != nullptr) o.route_counts[tid] += tot;
+    }
+  }
+  __syncthreads();
+
+  // 3. rows of this lane's entries
+  const int t = lane >> 2, g = lane & 3;
+  if (t0 + t < n_tokens) {
+    const int64_t f = (t0 + t) * KC + g * 2;
+    int row[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int e = sel[h];
+      row[h] = -1;
+      if (e >= 0) {
+        int r = s_base[e] + rank[h];
+        for (int ww = 0; ww < wave; ++ww) r += s_wcnt[ww][e];
+        row[h] = r;
+        o.perm[r] = static_cast<int32_t>(f + h);
+      }
+    }
+    o.row_of_entry[f] = row[0];
+    o.row_of_entry[f + 1] = row[1];
+  }
+  if (tid == 0) {
+    o.flags[b] = 0u;
+    o.flags[nb + b] = s_flag;
+    if (b == 0) {
+      o.header[0] = static_cast<uint32_t>(nb);
+      // every row of this call has been seen, so every workgroup has read the epoch
+      if (nb > 1) store_dev(o.header + kEpochWord, epoch);
+    }
+  }
 }
 
 // Top-k + softmax of precomputed logits: one wave per `rows` tokens.
@@ -604,7 +847,60 @@ hipError_t launch_router(const void* x, const void* w, int64_t n, int hidden, in
   return hipGetLastError();
 }
 
+// Workgroups of route_dispatch32_kernel<NSEG> the current device holds at
+// once (its occupancy per CU times the CUs), looked up once per device and NSEG.
+constexpr int kMaxDevicesR = 64;
+std::atomic<int> g_resident[kMaxDevicesR][3];
+
+template <int NSEG>
+int resident_capacity() {
+  constexpr int slot = NSEG == 1 ? 0 : (NSEG == 2 ? 1 : 2);
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  const bool cache = dev >= 0 && dev < kMaxDevicesR;
+  if (cache) {
+    const int c = g_resident[dev][slot].load(std::memory_order_relaxed);
+    if (c != 0) return c > 0 ? c : 0;
+  }
+  int per_cu = 0, cap = -1;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, route_dispatch32_kernel<NSEG>, kWaves * 64, 0) ==
+          hipSuccess &&
+      per_cu > 0)
+    cap = per_cu * device_cu_count();
+  if (cache) g_resident[dev][slot].store(cap, std::memory_order_relaxed);
+  return cap > 0 ? cap : 0;
+}
+
+template <int NSEG>
+hipError_t launch_fused(const uint16_t* x, const uint16_t* w, int64_t n, int64_t* idx, uint16_t* gate, float* logits,
+                        const FusedDispatch& o, int n_blocks, hipStream_t stream) {
+  // workgroups wait for each other's rows: all of them must fit at once
+  if (n_blocks > 1 && n_blocks > resident_capacity<NSEG>()) return hipErrorNotSupported;
+  route_dispatch32_kernel<NSEG><<<n_blocks, kWaves * 64, 0, stream>>>(x, w, n, idx, gate, logits, o);
+  return hipGetLastError();
+}
+
 }  // namespace
+
+hipError_t launch_route_dispatch_fused(const void* x, const void* w, int64_t n, int hidden, int E, int k, int dtype,
+                                       int64_t* idx, void* gate, float* logits, int32_t* counts, int32_t* offsets,
+                                       int32_t* perm, int32_t* row_of_entry, int64_t* route_counts, uint64_t* rows,
+                                       uint32_t* header, uint32_t* flags, const uint8_t* valid, int n_blocks,
+                                       hipStream_t stream) {
+  if (dtype != MEP_DTYPE_BF16 || E != 32 || k != 8 || n_blocks < 1 ||
+      static_cast<int64_t>(n_blocks) * kWaves * kRowsPerWave < n)
+    return hipErrorNotSupported;
+  const FusedDispatch o{counts, offsets, perm, row_of_entry, route_counts, rows, header, flags, valid};
+  const uint16_t* xb = static_cast<const uint16_t*>(x);
+  const uint16_t* wb = static_cast<const uint16_t*>(w);
+  uint16_t* gb = static_cast<uint16_t*>(gate);
+  switch (hidden) {
+    case 1024: return launch_fused<1>(xb, wb, n, idx, gb, logits, o, n_blocks, stream);
+    case 2048: return launch_fused<2>(xb, wb, n, idx, gb, logits, o, n_blocks, stream);
+    case 4096: return launch_fused<4>(xb, wb, n, idx, gb, logits, o, n_blocks, stream);
+    default: return hipErrorNotSupported;
+  }
+}
 
 hipError_t launch_router_with_hist(const void* x, const void* w, int64_t n, int hidden, int E, int k, int dtype,
                                    int64_t* idx, void* gate, float* logits, int32_t* bc, uint32_t* header,

@@ -41,4 +41,4 @@ int device_cu_count() {
 
 extern "C" const char* mep_last_error(void) { return mep::g_last_error; }
 
-extern "C" int mep_abi_version(void) { return 3; }
+extern "C" int mep_abi_version(void) { return 4; }

@@ -47,6 +47,7 @@ def _stream(dev: torch.device) -> int:
 
 
 _QUEUES: dict[tuple[int, int], torch.Tensor] = {}
+_ROUTE_WS: dict[tuple[int, int], torch.Tensor] = {}
 
 
 def _tile_queue(dev: torch.device, max_rows: int, n_local: int) -> torch.Tensor:
@@ -61,6 +62,19 @@ def _tile_queue(dev: torch.device, max_rows: int, n_local: int) -> torch.Tensor:
     if q is None or q.numel() < need:
         q = _QUEUES[key] = torch.zeros(max(need, 64), dtype=torch.int32, device=dev)
     return q
+
+
+def _route_workspace(dev: torch.device, nbytes: int) -> torch.Tensor:
+    """Workspace of mep_route_dispatch for the current stream of ``dev``:
+    zero-filled here (its grid-barrier words must start at zero; every call
+    leaves them at zero), one per stream so that calls on different streams
+    never share it, and replaced by a larger zeroed one when a call needs
+    more bytes."""
+    key = (dev.index if dev.index is not None else torch.cuda.current_device(), _stream(dev))
+    ws = _ROUTE_WS.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = _ROUTE_WS[key] = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=dev)
+    return ws
 
 
 def experts_check(dev: torch.device | None = None) -> None:
@@ -222,7 +236,7 @@ def route_dispatch(x_flat: torch.Tensor, w_router: torch.Tensor, k: int, valid_m
     idx = torch.empty((n, k), dtype=torch.int64, device=dev)
     gate = torch.empty((n, k), dtype=x.dtype, device=dev)
     logits = torch.empty((n, e), dtype=torch.float32, device=dev) if return_logits else None
-    ws = torch.empty(max(L.mep_route_dispatch_workspace_size(n, e), 256), dtype=torch.uint8, device=dev)
+    ws = _route_workspace(dev, int(L.mep_route_dispatch_workspace_size(n, e)))
     nk = max(n * k, 1)
     counts = torch.empty(e, dtype=torch.int32, device=dev)
     offsets = torch.empty(e + 1, dtype=torch.int32, device=dev)

@@ -143,11 +143,16 @@ def test_router_fused_tied_logits(e):
 
 @pytest.mark.parametrize("n,e,dtype,masked", [(16384, 32, torch.bfloat16, False), (700, 32, torch.bfloat16, True),
                                               (63, 16, torch.float32, True), (1, 64, torch.bfloat16, False),
+                                              (32, 32, torch.bfloat16, True),      # one workgroup
+                                              (32768, 32, torch.bfloat16, True),   # 512 workgroups, 2 per CU
+                                              (32769, 32, torch.bfloat16, False),  # one more: two launches
                                               (40000, 32, torch.bfloat16, True),   # > 512 blocks: scanned
                                               (0, 32, torch.bfloat16, False)])
 def test_route_dispatch_equals_two_calls(n, e, dtype, masked):
-    """mep_route_dispatch (router kernel with histogram output + scatter) gives
-    the bits of mep_router_topk followed by mep_dispatch."""
+    """mep_route_dispatch (bf16 with 32 experts: one cooperative launch while
+    its workgroups fit on the GPU at once; otherwise the router kernel with
+    histogram output + scatter) gives the bits of mep_router_topk followed by
+    mep_dispatch."""
     banner(f"route_dispatch n={n} e={e} {dtype} masked={masked}")
     L = workloads.make_layer(max(n, 1), seed=n + e, zipf_s=1.2 if e == 32 else 0.0, n_experts=e)
     x = L.x[:n].to(dtype).to(DEV)
@@ -166,3 +171,113 @@ def test_route_dispatch_equals_two_calls(n, e, dtype, masked):
     assert torch.equal(d.counts, d2.counts) and torch.equal(d.offsets, d2.offsets)
     assert torch.equal(d.perm[:M], d2.perm[:M]) and torch.equal(d.row_of_entry[: n * 8], d2.row_of_entry[: n * 8])
     assert torch.equal(rc1, rc2)
+
+
+def _route_vs_two_calls(x, w, valid):
+    e = w.shape[0]
+    n = x.shape[0]
+    rc1 = torch.zeros(e, dtype=torch.int64, device=DEV)
+    rc2 = torch.zeros(e, dtype=torch.int64, device=DEV)
+    idx, gate, d = ops.route_dispatch(x, w, 8, valid, route_counts=rc1)
+    idx2, gate2 = ops.router_topk(x, w, 8)
+    d2 = ops.dispatch(idx2, valid, e, torch.zeros(e, 1, dtype=torch.int32, device=DEV),
+                      torch.ones(e, dtype=torch.int32, device=DEV), False, None, 0,
+                      torch.arange(e, dtype=torch.int32, device=DEV), e, route_counts=rc2)
+    M = int(d2.offsets[-1])
+    assert torch.equal(idx, idx2) and torch.equal(gate, gate2)
+    assert torch.equal(d.counts, d2.counts) and torch.equal(d.offsets, d2.offsets)
+    assert torch.equal(d.perm[:M], d2.perm[:M]) and torch.equal(d.row_of_entry[: n * 8], d2.row_of_entry[: n * 8])
+    assert torch.equal(rc1, rc2)
+    return d
+
+
+@pytest.mark.parametrize("hidden,n", [(2048, 3000), (4096, 1500), (4096, 64)])
+def test_route_dispatch_fused_wide_hidden(hidden, n):
+    """The fused route + dispatch at hidden 2048 and 4096 (two and four K
+    segments of W_r per workgroup) equals the two calls bit for bit, and the
+    stable grouping equals the oracle's."""
+    banner(f"route_dispatch fused hidden={hidden} n={n}")
+    g = torch.Generator().manual_seed(hidden + n)
+    x = torch.randn(n, hidden, generator=g).to(torch.bfloat16).to(DEV)
+    w = (0.02 * torch.randn(32, hidden, generator=g)).to(torch.bfloat16).to(DEV)
+    valid = (torch.rand(n, generator=g) < 0.9).to(DEV)
+    d = _route_vs_two_calls(x, w, valid)
+    idx = to_np(ops.router_topk(x, w, 8)[0])
+    vm = to_np(valid).astype(bool)
+    ref = O.dispatch(idx, vm, 32, np.zeros((32, 1), np.int64), np.ones(32, np.int64), np.zeros((1, 32), np.int64),
+                     [0, n], 0, np.arange(32))
+    M = int(ref["offsets"][-1])
+    assert to_np(d.counts).tolist() == ref["counts"].tolist()
+    assert to_np(d.offsets).tolist() == ref["offsets"].tolist()
+    assert to_np(d.perm)[:M].tolist() == ref["perm"].tolist()
+    assert to_np(d.row_of_entry)[: n * 8].tolist() == ref["row_of_entry"].tolist()
+
+
+def test_route_dispatch_graph_replay():
+    """Captured in a HIP graph (the fused launch, one workgroup and 64), every
+    replay equals the eager call, with eager calls on other inputs in
+    between (the epoch advances on every replay)."""
+    banner("route_dispatch graph replay")
+    g = torch.Generator().manual_seed(5)
+    for n in (32, 4096):
+        xs = [torch.randn(n, 1024, generator=g).to(torch.bfloat16).to(DEV) for _ in range(2)]
+        w = (0.02 * torch.randn(32, 1024, generator=g)).to(torch.bfloat16).to(DEV)
+        x = xs[0].clone()
+        ref = ops.route_dispatch(x, w, 8, check=False)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            ops.route_dispatch(x, w, 8, check=False)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=side):
+                out = ops.route_dispatch(x, w, 8, check=False)
+        torch.cuda.current_stream().wait_stream(side)
+        for rep in range(3):
+            x.copy_(xs[rep % 2])
+            want = ops.route_dispatch(x, w, 8, check=False)
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out[0], want[0]) and torch.equal(out[1], want[1]), (n, rep)
+            assert torch.equal(out[2].offsets, want[2].offsets) and torch.equal(out[2].perm, want[2].perm), (n, rep)
+        del ref
+
+
+def test_route_dispatch_epoch_and_reuse():
+    """The fused call's epoch (workspace header word 32) advances once per
+    call of more than one workgroup, and one zero-filled workspace serves
+    calls of different sizes in any order (fused, two-kernel and one-workgroup
+    calls interleaved) with the two calls' bits every time."""
+    banner("route_dispatch epoch and workspace reuse")
+    from miniep_amd import _lib
+    L = _lib.lib()
+    e, hid = 32, 1024
+    g = torch.Generator().manual_seed(11)
+    big = 40000
+    ws = torch.zeros(L.mep_route_dispatch_workspace_size(big, e), dtype=torch.uint8, device=DEV)
+    words = ws[:256].view(torch.int32)
+    w = (0.02 * torch.randn(e, hid, generator=g)).to(torch.bfloat16).to(DEV)
+    s = torch.cuda.current_stream().cuda_stream
+    epoch = 0
+    for n in (4096, 16384, 40000, 32, 4096, 700, 16384):
+        x = torch.randn(n, hid, generator=g).to(torch.bfloat16).to(DEV)
+        idx = torch.empty(n, 8, dtype=torch.int64, device=DEV)
+        gate = torch.empty(n, 8, dtype=torch.bfloat16, device=DEV)
+        counts = torch.empty(e, dtype=torch.int32, device=DEV)
+        offsets = torch.empty(e + 1, dtype=torch.int32, device=DEV)
+        perm = torch.empty(n * 8, dtype=torch.int32, device=DEV)
+        row = torch.empty(n * 8, dtype=torch.int32, device=DEV)
+        assert L.mep_route_dispatch(x.data_ptr(), w.data_ptr(), None, n, hid, e, 8, 1, idx.data_ptr(),
+                                    gate.data_ptr(), None, counts.data_ptr(), offsets.data_ptr(), perm.data_ptr(),
+                                    row.data_ptr(), None, ws.data_ptr(), ws.numel(), s) == 0
+        assert L.mep_dispatch_check(ws.data_ptr(), s) == 0
+        nb = (n + 63) // 64
+        if 1 < nb <= 512:
+            epoch += 1
+        assert int(words[32]) == epoch, (n, int(words[32]), epoch)
+        idx2, _ = ops.router_topk(x, w, 8)
+        d2 = ops.dispatch(idx2, None, e, torch.zeros(e, 1, dtype=torch.int32, device=DEV),
+                          torch.ones(e, dtype=torch.int32, device=DEV), False, None, 0,
+                          torch.arange(e, dtype=torch.int32, device=DEV), e)
+        assert torch.equal(idx, idx2) and torch.equal(offsets, d2.offsets), n
+        assert torch.equal(perm, d2.perm[: n * 8]) and torch.equal(row, d2.row_of_entry[: n * 8]), n

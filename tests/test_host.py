@@ -22,7 +22,7 @@ def test_library_exports_every_header_function():
     assert len(names) == 21
     for n in names:
         assert hasattr(L, n), n
-    assert L.mep_abi_version() == 3
+    assert L.mep_abi_version() == 4
     assert _lib.last_error() == ""
 
 
