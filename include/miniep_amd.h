@@ -113,6 +113,13 @@ int mep_topk_softmax(const float* logits, int64_t n_tokens, int32_t n_experts,
  * Invalid expert ids are dropped and recorded; kept entries of non-resident
  * experts are dropped and recorded (ep.py:230 asserts); mep_dispatch_check()
  * reports them.  Supported: 1 <= k <= 32, E <= 256, S <= 16, N*k < 2^31.
+ * When its ceil(N*k / 512) blocks fit on the device at once (and there are
+ * at most 512), the dispatch is ONE launch whose blocks exchange their
+ * per-expert counts through the workspace, tagged with an epoch kept in the
+ * workspace header: the workspace must be zero-filled once when it is
+ * allocated and then reused as is (calls of any size); calls that overlap in
+ * time (different streams) need different workspaces.  Otherwise it runs as
+ * a count launch and a scatter launch (and a prefix launch above 512 blocks).
  * ---------------------------------------------------------------------- */
 size_t mep_dispatch_workspace_size(int64_t n_tokens, int32_t top_k, int32_t n_experts,
                                    int32_t n_segments, const int64_t* seg_tokens /* host */);

@@ -73,6 +73,7 @@ struct DispatchParams {
   int64_t* rr_snap;     // [S * E]
   int32_t* bc;          // [nbl * E]
   int32_t* segtot;      // [n_seg * E], written by prefix_kernel
+  uint64_t* rows;       // [nbl * E] tagged per-block counts (one-launch dispatch)
   int scanned;          // 1: prefix_kernel turned bc into per-segment exclusive prefixes
   int nb, nbl, n_seg;
   int64_t seg_entry[kMaxSeg + 1];
@@ -110,18 +111,20 @@ __device__ __forceinline__ int floor_mod(int64_t rr, int R) {
 }
 
 // #{w' in [0, w) : (rr + w') mod R == j}, summed over the slots j this rank
-// holds (bit j of `mine`; R replicas; rrmod = rr mod R).  32-bit: w counts
-// the entries of one expert in one segment (< 2^31), and rr enters only
-// through rrmod, so no 64-bit division runs per entry.
+// holds (bit j of `mine`; R replicas; rrmod = rr mod R).  With w = q R + r,
+// each residue class c = (j - rr) mod R holds q + [c < r] of the w' < w, and
+// c < r exactly for the r slots j = rrmod, rrmod + 1, ... (mod R): so the sum
+// is popc(mine) q + popc(mine & those r slots), one division per call.
+// 32-bit: w counts the entries of one expert in one segment (< 2^31), and rr
+// enters only through rrmod.
+__device__ __forceinline__ uint32_t low_bits(int n) { return n >= 32 ? ~0u : ((1u << n) - 1u); }
 __device__ __forceinline__ int kept_before(uint32_t mine, int R, uint32_t w, int rrmod) {
-  int n = 0;
-  for (int j = 0; j < R; ++j) {
-    if (!((mine >> j) & 1u)) continue;
-    int c = j - rrmod;
-    if (c < 0) c += R;
-    if (w > static_cast<uint32_t>(c)) n += static_cast<int>((w - c - 1) / static_cast<uint32_t>(R)) + 1;
-  }
-  return n;
+  const uint32_t q = w / static_cast<uint32_t>(R);
+  const int r = static_cast<int>(w - q * static_cast<uint32_t>(R));
+  const int hi = rrmod + r;                      // slots rrmod .. hi - 1, wrapping past R
+  const uint32_t first = low_bits(hi < R ? hi : R) & ~low_bits(rrmod);
+  const uint32_t wrap = hi > R ? low_bits(hi - R) : 0u;
+  return __popc(mine) * static_cast<int>(q) + __popc(mine & (first | wrap));
 }
 
 __global__ __launch_bounds__(kThreads) void count_kernel(DispatchParams p) {
@@ -214,6 +217,68 @@ __global__ __launch_bounds__(kScanThreads) void prefix_kernel(DispatchParams p) 
 // LDS copy of the replica table in scatter_kernel when it has at most this many entries
 constexpr int kTabLds = 2048;
 
+// One-launch dispatch (scatter_kernel<true>): every block also does
+// count_kernel's work for its own entries, publishes its per-expert counts as
+// 64-bit words (tag << 32 | count) with device-scope (sc1) stores, and reads
+// every block's counts with device-scope loads, re-reading until each word
+// carries this call's tag: they give the segment totals and its own prefix
+// (the earlier blocks of its segment).  No counter, no atomic across blocks:
+// the tag is 2^31 | (the workspace's epoch word + 1), read by every block as
+// it starts and advanced by block 0 once it has read every block's counts (by
+// then every block has published, so every block has read the epoch).
+// Whatever else the dispatch leaves in a workspace (counts, flags, tables,
+// round-robin counters below 2^32) has a clear top bit in its high word, so a
+// workspace zero-filled once serves calls of any size.  All blocks must be
+// resident at once: the host launches it only when they fit.  A wait longer
+// than kTagPolls polls sets kFlagBarrier in the block's status word.
+constexpr int kEpochWord = 32;                   // header word of the epoch (its own 128-byte line)
+constexpr int kTagPolls = 1 << 20;
+
+__device__ __forceinline__ uint32_t load_dev(const uint32_t* q) {
+  return __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t load_dev(const uint64_t* q) {
+  return __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_dev(uint64_t* q, uint64_t v) {
+  __hip_atomic_store(q, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_dev(uint32_t* q, uint32_t v) {
+  __hip_atomic_store(q, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Reads the tagged words w[i * stride] for i in [0, n) (this thread's share:
+// i = first, first + step, ...), each re-read until it carries `tag`, and
+// calls use(i, count) for each.  Sets *bad after kTagPolls polls of a batch.
+template <typename Use>
+__device__ __forceinline__ void read_tagged(const uint64_t* w, int64_t stride, int first, int n, int step,
+                                            uint64_t tag, uint32_t* bad, Use use) {
+  constexpr int kBatch = 8;
+  for (int i0 = first; i0 < n; i0 += step * kBatch) {
+    uint64_t v[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int i = i0 + u * step;
+      v[u] = i < n ? load_dev(w + i * stride) : tag;
+    }
+    for (int it = 0;; ++it) {
+      bool stale = false;
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) stale |= (v[u] & ~0xffffffffull) != tag;
+      if (!stale) break;
+      if (it >= kTagPolls) { *bad = kFlagBarrier; break; }
+      __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u)
+        if ((v[u] & ~0xffffffffull) != tag) v[u] = load_dev(w + (i0 + u * step) * stride);
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u)
+      if (i0 + u * step < n) use(i0 + u * step, static_cast<int>(static_cast<uint32_t>(v[u])));
+  }
+}
+
+template <bool FUSED>
 __global__ __launch_bounds__(kThreads) void scatter_kernel(DispatchParams p) {
   __shared__ int segtot[kMaxSeg][kMaxExperts];   // entries of expert e in segment s
   // per-expert tables, copied once per block (every entry looks them up):
@@ -226,54 +291,137 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(DispatchParams p) {
   __shared__ int keptbase[kMaxExperts];           // kept entries of e in earlier segments
   __shared__ int loff[kMaxExperts];               // first row of e's local expert
   __shared__ int lcount[kMaxExperts];             // rows per local expert
+  __shared__ int lpre[kMaxExperts + 1];           // exclusive prefix of lcount
+  __shared__ int lwave[kMaxExperts / 64];
   __shared__ int wcnt[kThreads / 64][kMaxExperts + 1];
   __shared__ uint32_t flag;
+  __shared__ int s_cnt[FUSED ? kMaxExperts : 1];  // one launch: this block's entries per expert
+  __shared__ uint32_t cflag;                      // one launch: this block's count-pass flags
 
   const int b = blockIdx.x, tid = threadIdx.x;
   const int E = p.E;
   const int s = segment_of_block(p, b);
   int64_t f0, f1;
   block_range(p, b, s, f0, f1);
+  uint64_t tag = 0;
+  if constexpr (FUSED) {
+    // this call's tag; the load has long landed when the tag is first used
+    tag = static_cast<uint64_t>(0x80000000u | ((load_dev(p.header + kEpochWord) + 1u) & 0x7fffffffu)) << 32;
+    asm volatile("" ::: "memory");
+  }
   // this thread's entry (a block is one round of entries), loaded first so
   // that its latency overlaps the histogram pass below
   static_assert(kChunk == kThreads, "one entry per thread");
   const int64_t f = f0 + tid;
   int key = E;                                    // E: no expert (padding, masked or out of range)
-  bool dropped = false;
+  bool dropped = false, bad_id = false;
   if (f < f1) {
     const bool valid = p.valid == nullptr || p.valid[f / p.k] != 0;
     const int64_t e = p.topk_idx[f];
     if (valid && e >= 0 && e < E) key = static_cast<int>(e);
     else dropped = true;
+    bad_id = valid && (e < 0 || e >= E);
   }
 
-  // the per-expert tables: their loads go out with the entry's, before the first barrier
+  // the per-expert tables: every load goes out with the entry's, before the
+  // first barrier (one memory round trip); what derives from them is
+  // computed from LDS and registers after it
+  static_assert(kThreads >= kMaxExperts, "one expert per thread");
   const bool tab_lds = E * p.rmax <= kTabLds;
   if (tab_lds)
     for (int i = tid; i < E * p.rmax; i += kThreads) s_tab[i] = p.table[i];
-  for (int e = tid; e < E; e += kThreads) {
-    const int R = reps(p, e);
-    uint32_t mine = 0;
-    for (int j = 0; j < R && j < 32; ++j) mine |= (p.table[e * p.rmax + j] == p.my_rank ? 1u : 0u) << j;
-    s_R[e] = R;
-    s_mine[e] = mine;
-    s_g2l[e] = p.g2l[e];
+  const int my_nrep = tid < E ? p.n_rep[tid] : 1;
+  if (tid < E) {
+    s_R[tid] = my_nrep < 1 ? 1 : (my_nrep > p.rmax ? p.rmax : my_nrep);   // reps(): clamped to [1, rmax]
+    s_g2l[tid] = p.g2l[tid];
   }
-  if (p.has_rep)
-    for (int i = tid; i < p.n_seg * E; i += kThreads) s_rrmod[i] = floor_mod(p.rr_snap[i], reps(p, i % E));
+  // round-robin counters of (segment, expert) i = tid + u kThreads; one launch
+  // reads rr itself (block 0 updates it only after every block has read it)
+  constexpr int kRrPer = kMaxSeg * kMaxExperts / kThreads;
+  int64_t rr_v[kRrPer];
+  if (p.has_rep) {
+#pragma unroll
+    for (int u = 0; u < kRrPer; ++u) {
+      const int i = tid + u * kThreads;
+      rr_v[u] = i < p.n_seg * E ? (FUSED ? p.rr[i] : p.rr_snap[i]) : 0;
+    }
+  }
   for (int i = tid; i < p.n_seg * kMaxExperts; i += kThreads) segtot[i / kMaxExperts][i % kMaxExperts] = 0;
   for (int e = tid; e < E; e += kThreads) { pre[e] = 0; lcount[e] = 0; }
   for (int i = tid; i < (kThreads / 64) * (kMaxExperts + 1); i += kThreads)
     wcnt[i / (kMaxExperts + 1)][i % (kMaxExperts + 1)] = 0;
   if (tid == 0) flag = 0;
+  if constexpr (FUSED) {
+    for (int e = tid; e < E; e += kThreads) s_cnt[e] = 0;
+    if (tid == 0) cflag = 0;
+  }
+  __syncthreads();
+  if (tid < E) {
+    const int R = s_R[tid];
+    uint32_t mine = 0;
+    if (tab_lds)
+      for (int j = 0; j < R; ++j) mine |= (s_tab[tid * p.rmax + j] == p.my_rank ? 1u : 0u) << j;
+    else
+      for (int j = 0; j < R; ++j) mine |= (p.table[tid * p.rmax + j] == p.my_rank ? 1u : 0u) << j;
+    s_mine[tid] = mine;
+  }
+  if (p.has_rep) {
+#pragma unroll
+    for (int u = 0; u < kRrPer; ++u) {
+      const int i = tid + u * kThreads;
+      if (i < p.n_seg * E) s_rrmod[i] = floor_mod(rr_v[u], s_R[i % E]);
+    }
+  }
+  uint32_t tag_bad = 0u;
+  if constexpr (FUSED) {
+    if (b == 0) {
+      if (tid == 0) {
+        p.header[0] = static_cast<uint32_t>(p.nbl);
+        // cleared (and acknowledged) before this block publishes its counts,
+        // so before any block ORs into it
+        if (p.status != nullptr) store_dev(p.status, 0u);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      }
+      // every expert needs 1..rmax replicas (ep.py:21: each expert has an owner)
+      if (tid < E && (my_nrep < 1 || my_nrep > p.rmax)) atomicOr(&cflag, kFlagReplicas);
+    }
+    // count_kernel's pass over this block's entries
+    if (key < E) atomicAdd(&s_cnt[key], 1);
+    if (bad_id) atomicOr(&cflag, kFlagRange);
+    __syncthreads();
+    for (int e = tid; e < E; e += kThreads)
+      store_dev(p.rows + static_cast<int64_t>(b) * E + e, tag | static_cast<uint32_t>(s_cnt[e]));
+    // every block's counts: the segment totals, and my prefix (the earlier
+    // blocks of my segment)
+    const int parts = kThreads / E > 0 ? kThreads / E : 1;
+    const int e = tid % E, part = tid / E;
+    if (part < parts && tid < parts * E) {
+      int my_pre = 0;
+      int sg = 0, sg_end = p.seg_block[1], run = 0;   // this thread's rows come in increasing order
+      read_tagged(p.rows + e, E, part, p.nb, parts, tag, &tag_bad, [&](int bb, int c) {
+        while (bb >= sg_end) {
+          if (run) atomicAdd(&segtot[sg][e], run);
+          run = 0;
+          ++sg;
+          sg_end = p.seg_block[sg + 1];
+        }
+        run += c;
+        if (sg == s && bb < b) my_pre += c;
+      });
+      if (run) atomicAdd(&segtot[sg][e], run);
+      atomicAdd(&pre[e], my_pre);
+    }
+  }
   __syncthreads();
 
-  // 1. segment totals and my prefix: read from prefix_kernel's results, or
+  // 1. segment totals and my prefix: from the tagged counts above (one
+  // launch), read from prefix_kernel's results, or
   // summed here from the per-block histograms.  The
   // histogram loads of a thread are issued 8 at a time before any of them is
   // used (one L2 round trip per 8 blocks instead of one per block); with one
   // segment the total is summed in a register and added to LDS once.
-  if (p.scanned) {
+  if (FUSED) {
+  } else if (p.scanned) {
     for (int i = tid; i < p.n_seg * E; i += kThreads) segtot[i / E][i % E] = p.segtot[i];
     for (int e = tid; e < E; e += kThreads) pre[e] = b < p.nb ? p.bc[static_cast<int64_t>(b) * E + e] : 0;
   } else {
@@ -322,25 +470,44 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(DispatchParams p) {
     if (j >= 0 && j < p.n_local) lcount[j] = static_cast<int>(total);
   }
   __syncthreads();
+  // exclusive prefix of the local counts: a scan over the first 4 waves
+  {
+    const int lane = tid & 63, wv = tid >> 6;
+    int v = 0, incl = 0;
+    if (tid < kMaxExperts) {
+      v = tid < p.n_local ? lcount[tid] : 0;
+      incl = v;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const int y = __shfl_up(incl, d, 64);
+        if (lane >= d) incl += y;
+      }
+      if (lane == 63) lwave[wv] = incl;
+    }
+    __syncthreads();
+    if (tid < kMaxExperts) {
+      int add = 0;
+#pragma unroll
+      for (int w = 0; w < kMaxExperts / 64; ++w) add += w < wv ? lwave[w] : 0;
+      lpre[tid] = add + incl - v;
+      if (tid == kMaxExperts - 1) lpre[kMaxExperts] = add + incl;
+    }
+    __syncthreads();
+  }
   for (int e = tid; e < E; e += kThreads) {
     const int j = s_g2l[e];
-    int off = 0;
-    if (j >= 0 && j < p.n_local)
-      for (int jj = 0; jj < j; ++jj) off += lcount[jj];
-    loff[e] = off;
+    loff[e] = (j >= 0 && j < p.n_local) ? lpre[j] : 0;
   }
   if (b == 0) {
     for (int j = tid; j <= p.n_local; j += kThreads) {
-      int off = 0;
-      for (int jj = 0; jj < j; ++jj) off += lcount[jj];
-      p.offsets[j] = off;
+      p.offsets[j] = lpre[j];
       if (j < p.n_local) p.counts[j] = lcount[j];
     }
     for (int e = tid; e < E; e += kThreads) {
       int64_t tot = 0;
       for (int sg = 0; sg < p.n_seg; ++sg) {
         tot += segtot[sg][e];
-        if (p.has_rep) p.rr[sg * E + e] = p.rr_snap[sg * E + e] + segtot[sg][e];
+        if (p.has_rep) p.rr[sg * E + e] = (FUSED ? p.rr[sg * E + e] : p.rr_snap[sg * E + e]) + segtot[sg][e];
       }
       if (p.route_counts != nullptr) p.route_counts[e] += tot;
     }
@@ -366,7 +533,8 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(DispatchParams p) {
   __syncthreads();
   if (key < E) {
     int w = pre[key] + rank_w;
-    for (int ww = 0; ww < wave; ++ww) w += wcnt[ww][key];
+#pragma unroll
+    for (int ww = 0; ww < kThreads / 64; ++ww) w += ww < wave ? wcnt[ww][key] : 0;
     const int e = key;
     const int rrmod = p.has_rep ? s_rrmod[s * E + e] : 0;
     const int R = s_R[e];
@@ -387,20 +555,24 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(DispatchParams p) {
     }
     p.row_of_entry[f] = row;
   }
+  if (FUSED && tag_bad) atomicOr(&flag, tag_bad);
   __syncthreads();
   if (tid == 0) {
     p.flags[p.nbl + b] = flag;
+    if constexpr (FUSED) p.flags[b] = cflag;
     if (p.status != nullptr) {
-      const uint32_t f = flag | p.flags[b];         // this block's count and scatter flags
+      const uint32_t f = flag | (FUSED ? cflag : p.flags[b]);   // this block's count and scatter flags
       if (f != 0u) atomicOr(p.status, f);
     }
+    // every block's counts have been read, so every block has read the epoch
+    if (FUSED && b == 0) store_dev(p.header + kEpochWord, static_cast<uint32_t>(tag >> 32) & 0x7fffffffu);
   }
 }
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 struct WsLayout {
-  size_t header, flags, rr_snap, bc, segtot, total;
+  size_t header, flags, rr_snap, bc, segtot, rows, total;
 };
 
 WsLayout ws_layout(int nbl, int n_seg, int E) {
@@ -410,7 +582,8 @@ WsLayout ws_layout(int nbl, int n_seg, int E) {
   l.rr_snap = align_up(l.flags + sizeof(uint32_t) * 2 * nbl, 256);
   l.bc = align_up(l.rr_snap + sizeof(int64_t) * n_seg * E, 256);
   l.segtot = align_up(l.bc + sizeof(int32_t) * static_cast<size_t>(nbl) * E, 256);
-  l.total = align_up(l.segtot + sizeof(int32_t) * static_cast<size_t>(n_seg) * E, 256);
+  l.rows = align_up(l.segtot + sizeof(int32_t) * static_cast<size_t>(n_seg) * E, 256);
+  l.total = align_up(l.rows + sizeof(uint64_t) * static_cast<size_t>(nbl) * E, 256);
   return l;
 }
 
@@ -443,10 +616,11 @@ extern "C" size_t mep_dispatch_workspace_size(int64_t n_tokens, int32_t top_k, i
 namespace mep {
 
 // Static scratch of mep_dispatch_noalloc: the workspace of mep_dispatch
-// (header, flags, counter snapshot, per-block histograms, segment totals) in
-// a file-scope device array, one copy per GPU, held until the process ends.
-// Every call on a GPU reuses that GPU's copy; the kernels write every word
-// they later read, so nothing needs clearing between calls.
+// (header, flags, counter snapshot, per-block histograms, segment totals,
+// tagged counts) in a file-scope device array, one copy per GPU, held until
+// the process ends.  Device arrays start zero-filled, which is all the
+// one-launch dispatch asks of a workspace; every call on a GPU reuses that
+// GPU's copy and nothing needs clearing between calls.
 constexpr size_t kScratchBytes = size_t(2) << 20;
 __device__ __attribute__((aligned(256))) unsigned char dispatch_scratch[kScratchBytes];
 
@@ -474,6 +648,26 @@ int scratch_address(void** out) {
   }
   *out = ptr;
   return MEP_OK;
+}
+
+// Blocks of scatter_kernel<true> the current device holds at once (its
+// occupancy per CU times the CUs), looked up once per device.
+std::atomic<int> g_fused_cap[kMaxDevices];
+
+int fused_capacity() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  const bool cache = dev >= 0 && dev < kMaxDevices;
+  if (cache) {
+    const int c = g_fused_cap[dev].load(std::memory_order_relaxed);
+    if (c != 0) return c > 0 ? c : 0;
+  }
+  int per_cu = 0, cap = -1;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, scatter_kernel<true>, kThreads, 0) == hipSuccess &&
+      per_cu > 0)
+    cap = per_cu * device_cu_count();
+  if (cache) g_fused_cap[dev].store(cap, std::memory_order_relaxed);
+  return cap > 0 ? cap : 0;
 }
 
 // Shared body of mep_dispatch and mep_dispatch_noalloc.  workspace == NULL
@@ -548,14 +742,22 @@ int dispatch_impl(const char* fn, const int64_t* topk_idx, const uint8_t* valid_
   for (int s = 0; s <= n_segments; ++s) p.seg_entry[s] = seg_tokens[s] * top_k;
   for (int s = n_segments + 1; s <= kMaxSeg; ++s) { p.seg_entry[s] = p.seg_entry[n_segments]; p.seg_block[s] = p.nb; }
 
+  p.rows = reinterpret_cast<uint64_t*>(ws + l.rows);
+
   hipStream_t st = static_cast<hipStream_t>(stream);
+  // one launch when every block fits on the device at once
+  if (p.nb >= 1 && !p.scanned && p.nb <= fused_capacity()) {
+    scatter_kernel<true><<<p.nbl, kThreads, 0, st>>>(p);
+    MEP_CHECK_LAUNCH("mep_dispatch(one launch)");
+    return MEP_OK;
+  }
   count_kernel<<<p.nbl, kThreads, 0, st>>>(p);
   MEP_CHECK_LAUNCH("mep_dispatch(count)");
   if (p.scanned) {
     prefix_kernel<<<n_experts, kScanThreads, 0, st>>>(p);
     MEP_CHECK_LAUNCH("mep_dispatch(prefix)");
   }
-  scatter_kernel<<<p.nbl, kThreads, 0, st>>>(p);
+  scatter_kernel<false><<<p.nbl, kThreads, 0, st>>>(p);
   MEP_CHECK_LAUNCH("mep_dispatch(scatter)");
   return MEP_OK;
 }
@@ -612,10 +814,6 @@ __global__ void empty_route_kernel(int n_local, int32_t* counts, int32_t* offset
 }
 
 size_t route_tables_offset(const WsLayout& l) { return l.total; }
-// tagged histogram rows of the fused route + dispatch, after the tables
-size_t route_rows_offset(const WsLayout& l, int E) {
-  return route_tables_offset(l) + align_up(sizeof(int32_t) * 3 * E, 256);
-}
 
 WsLayout route_layout(int64_t n_tokens, int32_t n_experts, int* nb_out) {
   const int nb = static_cast<int>((n_tokens * 8 + kChunk - 1) / kChunk);
@@ -630,7 +828,7 @@ extern "C" size_t mep_route_dispatch_workspace_size(int64_t n_tokens, int32_t n_
   if (n_tokens < 0 || n_experts <= 0 || n_experts > kMaxExperts) return 0;
   int nb = 0;
   const WsLayout l = route_layout(n_tokens, n_experts, &nb);
-  return route_rows_offset(l, n_experts) + sizeof(uint64_t) * static_cast<size_t>(nb > 0 ? nb : 1) * n_experts;
+  return route_tables_offset(l) + align_up(sizeof(int32_t) * 3 * n_experts, 256);
 }
 
 extern "C" int mep_route_dispatch(const void* x, const void* w_router, const uint8_t* valid_mask, int64_t n_tokens,
@@ -671,7 +869,7 @@ extern "C" int mep_route_dispatch(const void* x, const void* w_router, const uin
   // the device at once
   hipError_t e = launch_route_dispatch_fused(x, w_router, n_tokens, hidden, n_experts, top_k, dtype, topk_idx,
                                              topk_gate, logits, counts, offsets, perm, row_of_entry, route_counts,
-                                             reinterpret_cast<uint64_t*>(ws + route_rows_offset(l, n_experts)),
+                                             reinterpret_cast<uint64_t*>(ws + l.rows),
                                              reinterpret_cast<uint32_t*>(ws + l.header),
                                              reinterpret_cast<uint32_t*>(ws + l.flags), valid_mask, nb, st);
   if (e == hipSuccess) return MEP_OK;
@@ -708,7 +906,7 @@ extern "C" int mep_route_dispatch(const void* x, const void* w_router, const uin
     prefix_kernel<<<n_experts, kScanThreads, 0, st>>>(p);
     MEP_CHECK_LAUNCH("mep_route_dispatch(prefix)");
   }
-  scatter_kernel<<<p.nbl, kThreads, 0, st>>>(p);
+  scatter_kernel<false><<<p.nbl, kThreads, 0, st>>>(p);
   MEP_CHECK_LAUNCH("mep_route_dispatch(scatter)");
   return MEP_OK;
 }

@@ -770,7 +770,8 @@ __global__ __launch_bounds__(kWaves * 64) void route_dispatch32_kernel(const uin
       row[h] = -1;
       if (e >= 0) {
         int r = s_base[e] + rank[h];
-        for (int ww = 0; ww < wave; ++ww) r += s_wcnt[ww][e];
+#pragma unroll
+        for (int ww = 0; ww < kWaves; ++ww) r += ww < wave ? s_wcnt[ww][e] : 0;
         row[h] = r;
         o.perm[r] = static_cast<int32_t>(f + h);
       }

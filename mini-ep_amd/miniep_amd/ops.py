@@ -47,7 +47,7 @@ def _stream(dev: torch.device) -> int:
 
 
 _QUEUES: dict[tuple[int, int], torch.Tensor] = {}
-_ROUTE_WS: dict[tuple[int, int], torch.Tensor] = {}
+_DISPATCH_WS: dict[tuple[int, int], torch.Tensor] = {}
 
 
 def _tile_queue(dev: torch.device, max_rows: int, n_local: int) -> torch.Tensor:
@@ -64,16 +64,17 @@ def _tile_queue(dev: torch.device, max_rows: int, n_local: int) -> torch.Tensor:
     return q
 
 
-def _route_workspace(dev: torch.device, nbytes: int) -> torch.Tensor:
-    """Workspace of mep_route_dispatch for the current stream of ``dev``:
-    zero-filled here (its grid-barrier words must start at zero; every call
-    leaves them at zero), one per stream so that calls on different streams
-    never share it, and replaced by a larger zeroed one when a call needs
-    more bytes."""
+def _dispatch_workspace(dev: torch.device, nbytes: int) -> torch.Tensor:
+    """Workspace of mep_dispatch / mep_route_dispatch for the current stream
+    of ``dev``: zero-filled once here (the one-launch kernels keep the epoch
+    that tags the per-block counts they exchange in it), then reused as is by
+    every call on that stream, one per stream so that calls on different
+    streams never share it, and replaced by a larger zeroed one when a call
+    needs more bytes."""
     key = (dev.index if dev.index is not None else torch.cuda.current_device(), _stream(dev))
-    ws = _ROUTE_WS.get(key)
+    ws = _DISPATCH_WS.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = _ROUTE_WS[key] = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=dev)
+        ws = _DISPATCH_WS[key] = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=dev)
     return ws
 
 
@@ -188,8 +189,7 @@ def dispatch(topk_idx: torch.Tensor, valid_mask: torch.Tensor | None, n_experts:
     if route_counts is not None and (route_counts.dtype != torch.int64 or route_counts.numel() != n_experts):
         raise TypeError("route_counts must be an int64 tensor of n_experts")
     L = _lib.lib()
-    ws_bytes = L.mep_dispatch_workspace_size(n, k, n_experts, n_seg, seg_arr)
-    ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
+    ws = _dispatch_workspace(dev, int(L.mep_dispatch_workspace_size(n, k, n_experts, n_seg, seg_arr)))
     nk = max(n * k, 1)
     counts = torch.empty(max(n_local, 1), dtype=torch.int32, device=dev)
     offsets = torch.empty(n_local + 1, dtype=torch.int32, device=dev)
@@ -236,7 +236,7 @@ def route_dispatch(x_flat: torch.Tensor, w_router: torch.Tensor, k: int, valid_m
     idx = torch.empty((n, k), dtype=torch.int64, device=dev)
     gate = torch.empty((n, k), dtype=x.dtype, device=dev)
     logits = torch.empty((n, e), dtype=torch.float32, device=dev) if return_logits else None
-    ws = _route_workspace(dev, int(L.mep_route_dispatch_workspace_size(n, e)))
+    ws = _dispatch_workspace(dev, int(L.mep_route_dispatch_workspace_size(n, e)))
     nk = max(n * k, 1)
     counts = torch.empty(e, dtype=torch.int32, device=dev)
     offsets = torch.empty(e + 1, dtype=torch.int32, device=dev)

@@ -28,7 +28,7 @@ def _moe_layer_raw(L, x, w_r, w_in, w_out, k=8):
     ok(L.mep_router_topk(x.data_ptr(), w_r.data_ptr(), N, H, E, k, BF16, idx.data_ptr(), gate.data_ptr(),
                          None, s))
     seg = (i64 * 2)(0, N)
-    ws = torch.empty(L.mep_dispatch_workspace_size(N, k, E, 1, seg), dtype=torch.uint8, device="cuda")
+    ws = torch.zeros(L.mep_dispatch_workspace_size(N, k, E, 1, seg), dtype=torch.uint8, device="cuda")
     table = torch.zeros(E, 1, dtype=torch.int32, device="cuda")
     n_rep = torch.ones(E, dtype=torch.int32, device="cuda")
     g2l = torch.arange(E, dtype=torch.int32, device="cuda")

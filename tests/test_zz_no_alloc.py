@@ -37,7 +37,7 @@ def _call(L, noalloc, idx, table, n_rep, has_rep, rr, seg, my_rank, g2l, n_local
         rc = L.mep_dispatch_noalloc(*common, None if status is None else status.data_ptr(), s)
         assert rc == 0, L.mep_last_error()
         return None
-    ws = torch.empty(L.mep_dispatch_workspace_size(n, k, E, len(seg) - 1, segs), dtype=torch.uint8, device=DEV)
+    ws = torch.zeros(L.mep_dispatch_workspace_size(n, k, E, len(seg) - 1, segs), dtype=torch.uint8, device=DEV)
     rc = L.mep_dispatch(*common, ws.data_ptr(), ws.numel(), s)
     assert rc == 0, L.mep_last_error()
     return ws
