@@ -555,24 +555,20 @@ __device__ __forceinline__ void buffer_lds_16(const unsigned char* base, int byt
       (__attribute__((address_space(3))) void*)lds, 16, voff, __builtin_amdgcn_readfirstlane(soff), 0, 0);
 }
 
-// Hardware id of the XCD this wave runs on (0..7 on an 8-XCD part).
-__device__ __forceinline__ int xcc_id() {
-  unsigned v;
-  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
-  return static_cast<int>(v & 15u);
-}
-
 // Grouped GEMM over 256-row tiles of the dispatched rows: GEMM-1 + SwiGLU
 // (MODE kModeGateUp), GEMM-2 + scatter (kModeDown), or both in one launch
 // (kModeBoth).  Tiles are (row tile, column tile) pairs; a row tile is 256
 // consecutive rows of one expert (an expert's last one may be partial).
 //
 // Queues.  The row tiles are split into n_queues contiguous ranges, one per
-// XCD, and the workgroups of an XCD (read from the hardware, not assumed
-// from the workgroup id) take that range's tiles in order, one at a time,
-// through the XCD's counter in `sched`: the tiles of one expert run on one
-// XCD and share its weights in that XCD's L2, and the column tiles of a row
-// tile, taken one after the other, share the row tile's A rows there.  The
+// XCD, and the workgroups of an XCD take that range's tiles in order: the
+// first without a claim (workgroup b takes item b / n_queues of queue
+// b % n_queues; workgroups are dispatched to the XCDs round robin, so that is
+// b's XCD's queue, which matters only for L2 locality), the rest one at a
+// time through the queue's counter in `sched`, past those fixed slots.  The
+// tiles of one expert run on one XCD and share its weights in that XCD's L2,
+// and the column tiles of a row tile, taken one after the other, share the
+// row tile's A rows there.  The
 // XCDs do not run at one speed (the same work takes up to 8 % longer on one
 // than on another), so a workgroup whose queue is drained takes the
 // remaining tiles of the other queues (a bit per drained queue in `sched`
@@ -590,7 +586,8 @@ __device__ __forceinline__ int xcc_id() {
 // tile's first stages; if it is not met there, the workgroup finishes its tile, counts it, and
 // waits between tiles with nothing of its own pending: a workgroup that waits
 // holds no unfinished tile, and the tiles it waits for come earlier in the
-// queue than the one it waits with, so every wait ends.  A wait that still
+// queue than the one it waits with (fixed slots come before claimed ones),
+// so every wait ends.  A wait that still
 // exceeds sched::kWaitLimit polls sets sched flag kFlagWait and goes on.
 // Which workgroup computes a tile never changes its result, so the bits are
 // those of two separate launches.
@@ -648,6 +645,16 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(MoeParams p) {
   const int n1 = p.I / (BN / 2), n2 = p.H / BN;  // column tiles of a row tile: GEMM-1, GEMM-2
   int* const sched = p.sched;
 
+  // First items need no claim: workgroup b takes item b / nq of queue b % nq.
+  // Workgroups are dispatched to the XCDs round robin, so queue b % nq is
+  // b's XCD's (which only matters for L2 locality); every other item is
+  // claimed from a queue's counter, past the queue's n_static fixed slots.
+  const int nq = p.n_queues;
+  const int q = static_cast<int>(blockIdx.x) & (nq - 1);
+  const int n_static = static_cast<int>(gridDim.x) / nq;   // the grid is a multiple of nq
+  const int first_pos = static_cast<int>(blockIdx.x) / nq;
+  auto claim = [&](int qq) { return n_static + atomic_add_1(sched + sched::kQueue + qq, 1); };
+
   // ---- row tiles ------------------------------------------------------------------
   for (int j = tid; j <= nl; j += NT) s_off[j] = p.offsets[j];
   for (int j = tid; j < nl; j += NT) s_slot[j] = p.w_slot != nullptr ? p.w_slot[j] : j;
@@ -664,8 +671,6 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(MoeParams p) {
   // ---- queues ---------------------------------------------------------------------
   // Queue qq holds row tiles [lo(qq), lo(qq + 1)); a workgroup starts on its
   // XCD's queue and, when that is drained, takes tiles from the others.
-  const int nq = p.n_queues;
-  const int q = __builtin_amdgcn_readfirstlane(xcc_id() & (nq - 1));
   constexpr int kPerRowMode = MODE == kModeGateUp ? 1 : (MODE == kModeDown ? 2 : 3);
   const int per_row = kPerRowMode == 1 ? n1 : (kPerRowMode == 2 ? n2 : n1 + n2);
   auto q_lo = [&](int qq) { return static_cast<int>(static_cast<int64_t>(RT) * qq / nq); };
@@ -1013,6 +1018,7 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(MoeParams p) {
   int n_done = 0;
   int sig_r = -1;                                  // row tile of a GEMM-1 tile not yet counted
   int cq = q;                                      // the queue of the items in hand
+  bool first_round = true;
   for (;;) {
     // every wave waited for its stores (vmcnt(0)) before leaving the tile
     // loop: count the last GEMM-1 tile, then take two items
@@ -1020,17 +1026,35 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(MoeParams p) {
     if (tid == 0) {
       if (BOTH && sig_r >= 0) atomic_add_1(sched + sched::kRowDone + sig_r, 1);
       int a = INT_MAX, b = INT_MAX, qq = cq;
-      const int drained = atomic_read(sched + sched::kDrained);
-      for (int v = 0; v < nq; ++v) {
+      bool claimed = false;
+      if (first_round) {
+        // the fixed first item, and a second one as below; without one
+        // (n_static > n) the queue has nothing left to claim
+        const int n = q_items(q);
+        qq = q;
+        if (first_pos < n) {
+          a = first_pos;
+          const bool g2 = MODE == kModeDown || (BOTH && a >= (q_lo(q + 1) - q_lo(q)) * n1);
+          if (!g2) {
+            b = claim(q);
+            if (b >= n) atomic_or_1(sched + sched::kDrained, 1 << q);
+          }
+          claimed = true;
+        } else {
+          atomic_or_1(sched + sched::kDrained, 1 << q);
+        }
+      }
+      const int drained = claimed ? 0 : atomic_read(sched + sched::kDrained);
+      for (int v = 0; v < nq && !claimed; ++v) {
         qq = (cq + v) & (nq - 1);
         if ((drained >> qq) & 1) continue;
         const int n = q_items(qq);
-        a = atomic_add_1(sched + sched::kQueue + qq, 1);
+        a = claim(qq);
         if (a < n) {
           // a second item only while this one is a GEMM-1 tile (see the claims below)
           const bool g2 = MODE == kModeDown || (BOTH && a >= (q_lo(qq + 1) - q_lo(qq)) * n1);
           if (!g2) {
-            b = atomic_add_1(sched + sched::kQueue + qq, 1);
+            b = claim(qq);
             if (b >= n) atomic_or_1(sched + sched::kDrained, 1 << qq);
           }
           break;
@@ -1043,26 +1067,39 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(MoeParams p) {
       s_msg[3] = qq;
     }
     sig_r = -1;
+    first_round = false;
     __syncthreads();
     const int i0 = __builtin_amdgcn_readfirstlane(s_msg[0]), i1 = __builtin_amdgcn_readfirstlane(s_msg[1]);
     cq = __builtin_amdgcn_readfirstlane(s_msg[3]);
     const int n_items = q_items(cq);
     if (i0 >= n_items) break;                      // every queue is drained
-    int* const q_ctr = sched + sched::kQueue + cq;
 
     Tile cur = decode(i0, cq);
     bool has_next = i1 < n_items;
     Tile nxt = has_next ? decode(i1, cq) : cur;
+    // the weight waves load their first two stages at once (weight rows need
+    // neither the row map nor GEMM-1's rows); the A waves after the row map
+    // has landed (and, for a GEMM-2 tile, its rows are done)
+    Src sc;
+    if (!wave_a) {
+      sc = setup(cur, 0);
+#pragma unroll
+      for (int i = 0; i < BPW; ++i) dma_blk(sc, 0, 0, i);
+#pragma unroll
+      for (int i = 0; i < BPW; ++i) dma_blk(sc, 1, 1, i);
+    }
     if (BOTH && !cur.g1 && tid == 0) wait_rows(cur.R);
     rowmap_dma(cur, 0);
     if (has_next) rowmap_dma(nxt, 1);
     __builtin_amdgcn_s_waitcnt(kVmcnt0);
     __syncthreads();
-    Src sc = setup(cur, 0);
+    if (wave_a) {
+      sc = setup(cur, 0);
 #pragma unroll
-    for (int i = 0; i < BPW; ++i) dma_blk(sc, 0, 0, i);
+      for (int i = 0; i < BPW; ++i) dma_blk(sc, 0, 0, i);
 #pragma unroll
-    for (int i = 0; i < BPW; ++i) dma_blk(sc, 1, 1, i);
+      for (int i = 0; i < BPW; ++i) dma_blk(sc, 1, 1, i);
+    }
     __builtin_amdgcn_s_waitcnt(kVmcnt0);
     lds_barrier();
 
@@ -1098,7 +1135,7 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(MoeParams p) {
       sig_r = -1;
       int got = INT_MAX, dep = 0;
       if (tid == 0 && early) {
-        if (ahead2 || ahead1) got = atomic_add_1(q_ctr, 1);
+        if (ahead2 || ahead1) got = claim(cq);
         if (poll) dep = atomic_read(sched + sched::kRowDone + nxt.R);
       }
       step(S1, NO, YES, YES, sc, 2, 0, 1, act);          // step 1: DMA stage 2 -> buffer 0
@@ -1112,7 +1149,7 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(MoeParams p) {
       for (int k4 = 4; k4 < KT - 4; k4 += 4) {
         const bool late = k4 == KT - 8;
         if (tid == 0 && late) {
-          if (ahead2 || ahead1) got = atomic_add_1(q_ctr, 1);
+          if (ahead2 || ahead1) got = claim(cq);
           if (poll) dep = atomic_read(sched + sched::kRowDone + nxt.R);
         }
         step(S0, NO, NO, YES, sc, 0, 0, 0, act);
