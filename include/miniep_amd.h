@@ -213,14 +213,17 @@ int mep_route_dispatch(const void* x, const void* w_router, const uint8_t* valid
  * Supported: H % 256 == 0, I % 128 == 0.
  * With bf16, I % 256 == 0 and more than 2048 rows, both GEMMs run as ONE
  * persistent launch: each XCD works through its share of the row tiles, and
- * a row tile's GEMM-2 tiles start once its GEMM-1 tiles are done.
+ * a row tile's GEMM-2 tiles start once its GEMM-1 tiles are done.  With at
+ * most 1024 rows (decode) both small-batch GEMMs also run as one launch:
+ * GEMM-2's workgroups load their weights while GEMM-1 runs and start on a
+ * 32-row chunk once its GEMM-1 workgroups are done.
  * tile_queue: tile_queue_ints >= mep_experts_queue_ints(max_rows, n_local)
- * int32 of device memory, zero before the first call; the tiled kernels keep
- * their schedule there (per-XCD tile counters, per-row-tile GEMM-1
- * completion counts) and every launch leaves it zero again, except word 10:
- * sticky error flags that mep_experts_check reports (a GEMM-2 tile that gave
- * up waiting for its rows after about a second, a queue that no workgroup
- * drained; either means the results are invalid).  Launches that may run at
+ * int32 of device memory, zero before the first call; the one-launch kernels
+ * keep their schedule there (per-XCD tile counters, per-row-tile or
+ * per-chunk GEMM-1 completion counts) and every launch leaves it zero again,
+ * except word 10: sticky error flags that mep_experts_check reports (a
+ * GEMM-2 tile that gave up waiting for its rows after about a second, a
+ * queue that no workgroup drained; either means the results are invalid).  Launches that may run at
  * the same time (on different streams) need different queues; launches on
  * one stream can share one.  No counterpart in the reference (its experts
  * are a Python loop).

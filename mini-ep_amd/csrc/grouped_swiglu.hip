@@ -499,8 +499,16 @@ namespace sched {
 constexpr int kQueue = 0, kDone = 8, kItems = 9, kFlags = 10, kDrained = 11, kRowDone = 16;
 constexpr int kFlagWait = 1, kFlagDrain = 2;
 constexpr int kWaitLimit = 1 << 20;            // polls of one row counter (about a second)
-// row tiles of max_rows rows over n_local experts: each expert adds at most one partial tile
-inline int64_t words(int64_t max_rows, int n_local) { return kRowDone + (max_rows + 255) / 256 + n_local; }
+// the small-batch launch of both GEMMs runs up to this many rows
+constexpr int64_t kSmallRows = 1024;
+// row tiles of max_rows rows over n_local experts: each expert adds at most
+// one partial tile; the small-batch launch of both GEMMs keeps two words per
+// 32-row chunk there instead
+inline int64_t words(int64_t max_rows, int n_local) {
+  const int64_t tiles = (max_rows + 255) / 256 + n_local;
+  const int64_t chunks = max_rows <= kSmallRows ? (max_rows + 31) / 32 + n_local : 0;
+  return kRowDone + (tiles > 2 * chunks ? tiles : 2 * chunks);
+}
 }  // namespace sched
 
 constexpr int kModeGateUp = 1, kModeDown = 2, kModeBoth = 3;
@@ -1280,15 +1288,25 @@ constexpr int DEPTH = 8;                      // K-steps of loads in flight
 // use this path when N * k is at most this (measured crossover against the
 // tiled kernel: GEMM-1 between 1024 and 2048 entries, GEMM-2 past 2048)
 constexpr int64_t kMaxEntries1 = 1024, kMaxEntries2 = 2048;
+static_assert(kMaxEntries1 == sched::kSmallRows, "schedule words of the small-batch launch");
 }  // namespace skinny
 
-template <bool GEMM1>
-__global__ __launch_bounds__(skinny::NT) void moe_gemm_skinny_kernel(GemmParams p) {
+// One workgroup's share of a small-batch GEMM: chunk `block / n_cb`, column
+// block `block % n_cb`.  FUSED (both GEMMs in one launch, GEMM-1's workgroups
+// first in the grid): GEMM-1 writes act with device-scope stores and, once
+// they are complete, adds one to its chunk's counter in `sched`; GEMM-2 loads
+// its first DEPTH steps of weights, then thread 0 waits (bounded) until the
+// chunk's counter shows every GEMM-1 column block, and only then are act's
+// rows loaded.  The workgroups are dispatched in grid order, so every GEMM-1
+// workgroup is resident before any GEMM-2 workgroup can wait, and every wait
+// ends.  The last GEMM-2 workgroup of a chunk to pass the wait returns its
+// two counters to zero.
+template <bool GEMM1, bool FUSED>
+__device__ __forceinline__ void skinny_body(const GemmParams& p, int block, int n_cb_other, int* sched,
+                                            int* s_pre, int* s_off) {
   using namespace skinny;
   typedef uint16_t T;
   constexpr int CH = 16 * MFC;                                // rows per workgroup
-  __shared__ int s_pre[bfk::NLMAX + 1];                       // chunks before expert j
-  __shared__ int s_off[bfk::NLMAX + 1];
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nl = p.n_local;
   // chunk table: expert j owns ceil(rows_j / CH) chunks of CH rows; workgroup
@@ -1299,8 +1317,9 @@ __global__ __launch_bounds__(skinny::NT) void moe_gemm_skinny_kernel(GemmParams 
   if (tid < 64) scan_units<CH>(s_off, s_pre, nl, 1);
   __syncthreads();
   const int n_cb = GEMM1 ? p.N / 64 : p.N / 128;             // column blocks per expert
-  const int q = blockIdx.x / n_cb, cb = blockIdx.x % n_cb;
-  if (q >= s_pre[nl]) return;
+  const int q = block / n_cb, cb = block % n_cb;
+  const int n_chunks = s_pre[nl];
+  if (q >= n_chunks) return;
   int lo = 0, hi = nl - 1;                                    // largest j with s_pre[j] <= q
   while (lo < hi) {
     const int mid = (lo + hi + 1) >> 1;
@@ -1331,9 +1350,43 @@ __global__ __launch_bounds__(skinny::NT) void moe_gemm_skinny_kernel(GemmParams 
   const T* wp1 = W + static_cast<int64_t>(wrow[1]) * K + 8 * lg;
   const T* A = static_cast<const T*>(p.A);
   T* const C = static_cast<T*>(p.C);
+  // chunk counters of the fused launch: GEMM-1 workgroups done, GEMM-2 workgroups past the wait
+  int* const done1 = FUSED ? sched + sched::kRowDone + 2 * q : nullptr;
+  int* const seen2 = FUSED ? done1 + 1 : nullptr;
 
   {
     const int r0 = row_lo;
+    u32x4 wq[DEPTH][2], aq[DEPTH][MFC];
+    auto k_off = [&](int t) {
+      int ks = t + rot;
+      if (ks >= KT) ks -= KT;
+      return static_cast<int64_t>(ks) * 32;
+    };
+    auto load_w = [&](int t, int slot) {
+      const int64_t off = k_off(t);
+      wq[slot][0] = *reinterpret_cast<const u32x4*>(wp0 + off);
+      wq[slot][1] = *reinterpret_cast<const u32x4*>(wp1 + off);
+    };
+    if constexpr (FUSED && !GEMM1) {
+      // the weights do not depend on GEMM-1: their first steps go out before the wait
+#pragma unroll
+      for (int d = 0; d < DEPTH; ++d) load_w(d, d);
+      if (tid == 0) {
+        int polls = 0;
+        while (atomic_read(done1) < n_cb_other) {
+          if (++polls == sched::kWaitLimit) {
+            atomic_or_1(sched + sched::kFlags, sched::kFlagWait);
+            break;
+          }
+          __builtin_amdgcn_s_sleep(2);
+        }
+        if (atomic_add_1(seen2, 1) == n_cb - 1) {
+          atomicExch(done1, 0);
+          atomicExch(seen2, 0);
+        }
+      }
+      __syncthreads();
+    }
     // A rows of the pass (rows past row_hi read the last row; never stored)
     const T* ap[MFC];
 #pragma unroll
@@ -1344,13 +1397,8 @@ __global__ __launch_bounds__(skinny::NT) void moe_gemm_skinny_kernel(GemmParams 
       else src = r;                                        // act row
       ap[f] = A + src * K + 8 * lg;
     }
-    u32x4 wq[DEPTH][2], aq[DEPTH][MFC];
-    auto load = [&](int t, int slot) {
-      int ks = t + rot;
-      if (ks >= KT) ks -= KT;
-      const int64_t off = static_cast<int64_t>(ks) * 32;
-      wq[slot][0] = *reinterpret_cast<const u32x4*>(wp0 + off);
-      wq[slot][1] = *reinterpret_cast<const u32x4*>(wp1 + off);
+    auto load_a = [&](int t, int slot) {
+      const int64_t off = k_off(t);
 #pragma unroll
       for (int f = 0; f < MFC; ++f) aq[slot][f] = *reinterpret_cast<const u32x4*>(ap[f] + off);
     };
@@ -1362,7 +1410,10 @@ __global__ __launch_bounds__(skinny::NT) void moe_gemm_skinny_kernel(GemmParams 
 #pragma unroll
       for (int j = 0; j < 2; ++j) acc[f][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int d = 0; d < DEPTH; ++d) load(d, d);
+    for (int d = 0; d < DEPTH; ++d) {
+      if constexpr (!(FUSED && !GEMM1)) load_w(d, d);
+      load_a(d, d);
+    }
     for (int t0 = 0; t0 < KT; t0 += DEPTH) {             // KT is a multiple of DEPTH
 #pragma unroll
       for (int d = 0; d < DEPTH; ++d) {
@@ -1370,7 +1421,10 @@ __global__ __launch_bounds__(skinny::NT) void moe_gemm_skinny_kernel(GemmParams 
         for (int f = 0; f < MFC; ++f)
 #pragma unroll
           for (int j = 0; j < 2; ++j) mfma_acc(acc[f][j], wq[d][j], aq[d][f]);
-        if (t0 + d + DEPTH < KT) load(t0 + d + DEPTH, d);
+        if (t0 + d + DEPTH < KT) {
+          load_w(t0 + d + DEPTH, d);
+          load_a(t0 + d + DEPTH, d);
+        }
       }
     }
     // results: lane (lr, lg) of fragment j holds columns 4 lg .. 4 lg + 3 of
@@ -1391,7 +1445,11 @@ __global__ __launch_bounds__(skinny::NT) void moe_gemm_skinny_kernel(GemmParams 
         for (int h = 0; h < 2; ++h)
           w[h] = pack_bf16x2(silu_f(acc[f][0][2 * h]) * acc[f][1][2 * h],
                              silu_f(acc[f][0][2 * h + 1]) * acc[f][1][2 * h + 1]);
-        *reinterpret_cast<uint2*>(C + static_cast<int64_t>(r) * p.N + col) = make_uint2(w[0], w[1]);
+        uint64_t* const dst = reinterpret_cast<uint64_t*>(C + static_cast<int64_t>(r) * p.N + col);
+        const uint64_t v = (static_cast<uint64_t>(w[1]) << 32) | w[0];
+        // fused: device scope, so GEMM-2 on any XCD reads the final rows
+        if constexpr (FUSED) __hip_atomic_store(dst, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else *dst = v;
       } else {
         const int64_t row = p.perm[r];                     // (token, slot) cell
 #pragma unroll
@@ -1403,6 +1461,30 @@ __global__ __launch_bounds__(skinny::NT) void moe_gemm_skinny_kernel(GemmParams 
       }
     }
   }
+  if constexpr (FUSED && GEMM1) {
+    // every wave's act stores are complete before the chunk's count goes up
+    __builtin_amdgcn_s_waitcnt(kVmcnt0);
+    __syncthreads();
+    if (tid == 0) atomic_add_1(done1, 1);
+  }
+}
+
+template <bool GEMM1>
+__global__ __launch_bounds__(skinny::NT) void moe_gemm_skinny_kernel(GemmParams p) {
+  __shared__ int s_pre[bfk::NLMAX + 1];                       // chunks before expert j
+  __shared__ int s_off[bfk::NLMAX + 1];
+  skinny_body<GEMM1, false>(p, blockIdx.x, 0, nullptr, s_pre, s_off);
+}
+
+// Both small-batch GEMMs in one launch: workgroups [0, g1_blocks) are GEMM-1's,
+// the rest GEMM-2's (see skinny_body).
+__global__ __launch_bounds__(skinny::NT) void moe_gemm_skinny_both_kernel(GemmParams p1, GemmParams p2,
+                                                                          int g1_blocks, int* sched) {
+  __shared__ int s_pre[bfk::NLMAX + 1];
+  __shared__ int s_off[bfk::NLMAX + 1];
+  const int b = blockIdx.x;
+  if (b < g1_blocks) skinny_body<true, true>(p1, b, p2.N / 128, sched, s_pre, s_off);
+  else skinny_body<false, true>(p2, b - g1_blocks, p1.N / 64, sched, s_pre, s_off);
 }
 
 template <bool GEMM1>
@@ -1413,6 +1495,16 @@ hipError_t launch_skinny(const GemmParams& p, int64_t max_rows, hipStream_t stre
   const int64_t blocks = chunks * n_cb;
   if (blocks == 0) return hipSuccess;
   moe_gemm_skinny_kernel<GEMM1><<<dim3(static_cast<unsigned>(blocks)), skinny::NT, 0, stream>>>(p);
+  return hipGetLastError();
+}
+
+hipError_t launch_skinny_both(const GemmParams& p1, const GemmParams& p2, int64_t max_rows, int* sched,
+                              hipStream_t stream) {
+  const int64_t chunks = (max_rows + 16 * skinny::MFC - 1) / (16 * skinny::MFC) + p1.n_local;
+  const int64_t b1 = chunks * (p1.N / 64), b2 = chunks * (p2.N / 128);
+  if (b1 + b2 == 0) return hipSuccess;
+  moe_gemm_skinny_both_kernel<<<dim3(static_cast<unsigned>(b1 + b2)), skinny::NT, 0, stream>>>(
+      p1, p2, static_cast<int>(b1), sched);
   return hipGetLastError();
 }
 
@@ -1469,6 +1561,34 @@ bool tiled_down(int dtype, int64_t max_rows, int inter) {
 typedef TileCfg<256, 256, 4, 2> CfgBf16;
 typedef TileCfg<128, 128, 2, 2> CfgF32;
 
+// GEMM-1 / GEMM-2 parameters of the small-batch and generic kernels
+template <int DT, class Cfg>
+GemmParams gemm1_params(const void* x, int64_t n_tokens, int top_k, const int32_t* perm, const int32_t* offsets,
+                        int n_local, const void* w_in, const int32_t* w_slot, int hidden, int inter, void* act) {
+  GemmParams g1;
+  g1.A = x; g1.perm = perm; g1.offsets = offsets; g1.W = w_in; g1.C = act;
+  g1.w_slot = w_slot;
+  g1.w_expert_stride = static_cast<int64_t>(2) * inter * hidden;
+  g1.n_local = n_local; g1.top_k = top_k; g1.K = hidden; g1.N = inter;
+  g1.n_tiles_n = inter / (Cfg::BN / 2);
+  g1.a_bytes = static_cast<uint32_t>(n_tokens * hidden * dtype_bytes(DT));
+  div_magic(static_cast<uint32_t>(top_k), &g1.k_magic, &g1.k_shift);
+  return g1;
+}
+template <int DT, class Cfg>
+GemmParams gemm2_params(const void* act, int top_k, const int32_t* perm, const int32_t* offsets, int n_local,
+                        int64_t max_rows, const void* w_out, const int32_t* w_slot, int hidden, int inter, void* y) {
+  GemmParams g2;
+  g2.A = act; g2.perm = perm; g2.offsets = offsets; g2.W = w_out; g2.C = y;
+  g2.w_slot = w_slot;
+  g2.w_expert_stride = static_cast<int64_t>(hidden) * inter;
+  g2.n_local = n_local; g2.top_k = top_k; g2.K = inter; g2.N = hidden;
+  g2.n_tiles_n = hidden / Cfg::BN;
+  g2.a_bytes = static_cast<uint32_t>(max_rows * inter * dtype_bytes(DT));
+  div_magic(static_cast<uint32_t>(top_k), &g2.k_magic, &g2.k_shift);
+  return g2;
+}
+
 template <int DT, class Cfg>
 int run_gate_up(const void* x, int64_t n_tokens, int top_k, const int32_t* perm, const int32_t* offsets,
                 int n_local, int64_t max_rows, const void* w_in, const int32_t* w_slot, int hidden, int inter,
@@ -1479,14 +1599,8 @@ int run_gate_up(const void* x, int64_t n_tokens, int top_k, const int32_t* perm,
                                    hidden, inter, act, nullptr, sched);
     e = launch_tiled<kModeGateUp>(p, max_rows, stream);
   } else {
-    GemmParams g1;
-    g1.A = x; g1.perm = perm; g1.offsets = offsets; g1.W = w_in; g1.C = act;
-    g1.w_slot = w_slot;
-    g1.w_expert_stride = static_cast<int64_t>(2) * inter * hidden;
-    g1.n_local = n_local; g1.top_k = top_k; g1.K = hidden; g1.N = inter;
-    g1.n_tiles_n = inter / (Cfg::BN / 2);
-    g1.a_bytes = static_cast<uint32_t>(n_tokens * hidden * dtype_bytes(DT));
-    div_magic(static_cast<uint32_t>(top_k), &g1.k_magic, &g1.k_shift);
+    const GemmParams g1 = gemm1_params<DT, Cfg>(x, n_tokens, top_k, perm, offsets, n_local, w_in, w_slot, hidden,
+                                                inter, act);
     if (DT == MEP_DTYPE_BF16) e = launch_skinny<true>(g1, max_rows, stream);
     else e = launch<DT, Cfg, true>(g1, max_rows, stream);
   }
@@ -1504,14 +1618,8 @@ int run_down(const void* act, int top_k, const int32_t* perm, const int32_t* off
                              inter, const_cast<void*>(act), y, sched);
     e = launch_tiled<kModeDown>(p, max_rows, stream);
   } else {
-    GemmParams g2;
-    g2.A = act; g2.perm = perm; g2.offsets = offsets; g2.W = w_out; g2.C = y;
-    g2.w_slot = w_slot;
-    g2.w_expert_stride = static_cast<int64_t>(hidden) * inter;
-    g2.n_local = n_local; g2.top_k = top_k; g2.K = inter; g2.N = hidden;
-    g2.n_tiles_n = hidden / Cfg::BN;
-    g2.a_bytes = static_cast<uint32_t>(max_rows * inter * dtype_bytes(DT));
-    div_magic(static_cast<uint32_t>(top_k), &g2.k_magic, &g2.k_shift);
+    const GemmParams g2 = gemm2_params<DT, Cfg>(act, top_k, perm, offsets, n_local, max_rows, w_out, w_slot, hidden,
+                                                inter, y);
     if (DT == MEP_DTYPE_BF16 && inter % 256 == 0) e = launch_skinny<false>(g2, max_rows, stream);
     else e = launch<DT, Cfg, false>(g2, max_rows, stream);
   }
@@ -1629,6 +1737,22 @@ int grouped_impl(const char* fn, const void* x, int64_t n_tokens, int32_t top_k,
     const MoeParams p = moe_params(x, n_tokens, top_k, perm, offsets, n_local, max_rows, w_in, w_out, w_slot,
                                    hidden, inter, workspace, y_entries, tile_queue);
     const hipError_t e = launch_tiled<kModeBoth>(p, max_rows, static_cast<hipStream_t>(stream));
+    MEP_REQUIRE(e == hipSuccess, MEP_ERR_HIP, "%s: %s", fn, hipGetErrorString(e));
+    return MEP_OK;
+  }
+  if (dtype == MEP_DTYPE_BF16 && inter % 256 == 0 && !tiled_gate_up(dtype, max_rows) &&
+      !tiled_down(dtype, max_rows, inter)) {
+    // both small-batch GEMMs in one launch (GEMM-2's weights stream while GEMM-1 runs)
+    MEP_REQUIRE(x && perm && offsets && w_in && w_out && y_entries, MEP_ERR_INVALID_ARG, "%s: null pointer", fn);
+    rc = check_queue(fn, true, tile_queue, tile_queue_ints, max_rows, n_local);
+    if (rc != MEP_OK) return rc;
+    MEP_REQUIRE(aligned16(x) && aligned16(w_in) && aligned16(w_out) && aligned16(workspace) && aligned16(y_entries),
+                MEP_ERR_INVALID_ARG, "%s: buffers must be 16-byte aligned", fn);
+    const GemmParams g1 = gemm1_params<MEP_DTYPE_BF16, CfgBf16>(x, n_tokens, top_k, perm, offsets, n_local, w_in,
+                                                                w_slot, hidden, inter, workspace);
+    const GemmParams g2 = gemm2_params<MEP_DTYPE_BF16, CfgBf16>(workspace, top_k, perm, offsets, n_local, max_rows,
+                                                                w_out, w_slot, hidden, inter, y_entries);
+    const hipError_t e = launch_skinny_both(g1, g2, max_rows, tile_queue, static_cast<hipStream_t>(stream));
     MEP_REQUIRE(e == hipSuccess, MEP_ERR_HIP, "%s: %s", fn, hipGetErrorString(e));
     return MEP_OK;
   }

@@ -219,6 +219,58 @@ def test_one_launch_equals_two_launches(case):
         assert (to_np(y1)[np.repeat(~valid.numpy(), k)] == 7.0).all()
 
 
+@pytest.mark.parametrize("case", ["decode_t32", "zipf_t128", "masked_t100", "e64_t16"])
+def test_small_batch_one_launch_equals_two_launches(case):
+    """Batches of at most 1024 (token, slot) entries run both small-batch
+    GEMMs as one launch (GEMM-2's workgroups load their weights, then wait
+    for their chunk's GEMM-1 workgroups).  Bits equal the two launches on
+    every row, other rows are left alone, the schedule words return to zero,
+    and consecutive calls on other inputs (the same act workspace) give each
+    input's own result."""
+    banner(f"experts small-batch one launch vs two: {case}")
+    bf = torch.bfloat16
+    g = torch.Generator().manual_seed(21)
+    E = 64 if case.startswith("e64") else 32
+    n = int(case.split("_t")[1])
+    valid = None
+    if case.startswith("zipf"):
+        L = workloads.make_layer(n, seed=21, zipf_s=1.2)
+        topk = (L.x @ L.w_router.T).topk(8, dim=-1).indices
+        x, w_in, w_out = L.x, L.w_in, L.w_out
+    else:
+        topk = torch.rand(n, E, generator=g).topk(8, -1).indices
+        x = torch.randn(n, 1024, generator=g)
+        w_in, w_out = workloads.expert_weights(g, E)
+        if case.startswith("masked"):
+            valid = torch.rand(n, generator=g) < 0.7
+    k = 8
+    table, n_rep, g2l = _world1(E)
+    d = ops.dispatch(topk.to(DEV), None if valid is None else valid.to(DEV), E, table, n_rep, False, None, 0, g2l, E)
+    if case == "zipf_t128":
+        assert int(d.counts.max()) > 32                    # an expert of several 32-row chunks
+    wi, wo = w_in.to(bf).to(DEV), w_out.to(bf).to(DEV)
+    results = []
+    for rep in range(2):                                   # a second input through the same buffers
+        xd = (x if rep == 0 else torch.randn(x.shape, generator=g)).to(bf).to(DEV)
+        y1 = torch.full((n * k, 1024), 7.0, dtype=bf, device=DEV)
+        y2 = y1.clone()
+        ops.grouped_swiglu(xd, d, wi, wo, y1)
+        _two_launches(xd, d, wi, wo, y2)
+        ops.experts_check()
+        assert torch.equal(y1, y2), rep
+        for q in ops._QUEUES.values():
+            assert int(q.abs().sum()) == 0
+        if valid is not None:
+            assert (to_np(y1)[np.repeat(~valid.numpy(), k)] == 7.0).all()
+        results.append(y1)
+    assert not torch.equal(results[0], results[1])
+    rows = np.repeat(np.arange(n), k)
+    keep = np.ones(n * k, bool) if valid is None else np.repeat(valid.numpy(), k)
+    ref = O.experts(xd.float().cpu().numpy()[rows[keep]], topk.numpy().reshape(-1)[keep], wi.float().cpu().numpy(),
+                    wo.float().cpu().numpy(), act_bf16=True, out_bf16=True)
+    assert rel_err(to_np(results[1])[keep], ref) <= TOL_BF16
+
+
 @pytest.mark.parametrize("stride", [128, 16])
 def test_small_batch_kernel_matches_main_kernel_bitwise(stride):
     """Batches of at most 2048 (token, slot) entries run the few-rows-per-expert
