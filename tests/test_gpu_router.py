@@ -213,6 +213,19 @@ def test_route_dispatch_fused_wide_hidden(hidden, n):
     assert to_np(d.row_of_entry)[: n * 8].tolist() == ref["row_of_entry"].tolist()
 
 
+@pytest.mark.parametrize("n", [32, 5000])
+def test_route_dispatch_fused_logits(n):
+    """The fused route + dispatch's optional fp32 logits output equals the
+    router's (one workgroup and many)."""
+    banner(f"route_dispatch fused logits n={n}")
+    g = torch.Generator().manual_seed(n)
+    x = torch.randn(n, 1024, generator=g).to(torch.bfloat16).to(DEV)
+    w = (0.02 * torch.randn(32, 1024, generator=g)).to(torch.bfloat16).to(DEV)
+    idx, gate, d, logits = ops.route_dispatch(x, w, 8, return_logits=True)
+    idx2, gate2, logits2 = ops.router_topk(x, w, 8, return_logits=True)
+    assert torch.equal(idx, idx2) and torch.equal(gate, gate2) and torch.equal(logits, logits2)
+
+
 def test_route_dispatch_graph_replay():
     """Captured in a HIP graph (the fused launch, one workgroup and 64), every
     replay equals the eager call, with eager calls on other inputs in
