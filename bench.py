@@ -205,7 +205,10 @@ def decode_detail(dev, calls: int = 200) -> dict:
             be.route_and_call(x, w_r, K)
     torch.cuda.current_stream().wait_stream(side)
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
+    # captured on the warmed-up stream: the library keeps its zero-filled
+    # workspaces per stream, and a first call inside the capture would record
+    # their one-time fill into every replay
+    with torch.cuda.graph(graph, stream=side):
         out = be.route_and_call(x, w_r, K)[0]
     replays_equal = True
     for _ in range(3):

@@ -974,39 +974,68 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(MoeParams p) {
       // as 4 rows x 256 contiguous bytes per store: whole 128-byte lines,
       // which the memory system takes about twice as fast as half lines.
       // The slice is private to the wave and a wave's LDS accesses complete
-      // in issue order, so no barrier or wait is needed around it.
-      T* const C = static_cast<T*>(p.y);
-      const int col0 = t.nt * BN + wn * 128;                              // the wave's first output column
-      unsigned char* const stg = smem + STG + wave * STG_WAVE;
+      // in issue order, so no barrier or wait is needed around it: round k
+      // (rows 8k .. 8k+7 of the wave's 64) writes the slice before round
+      // k-1's stores go out and reads it back after them, so the wait for a
+      // round's reads overlaps the next round's writes (the row map's
+      // destination cells are read with the round's data).  The output base
+      // is held in scalar registers (a kernel argument reloaded mid-epilogue
+      // is a scalar load, whose wait also waits for every LDS access in
+      // flight).
       const int lrow = (et >> 4) & 3, lchunk = et & 15;                    // read-back: row lrow (+4), chunk lchunk
+      unsigned char* const stg = smem + STG + wave * STG_WAVE;
+      uint64_t ybase = reinterpret_cast<uint64_t>(static_cast<T*>(p.y) + t.nt * BN + wn * 128);
+      uint32_t ystride = static_cast<uint32_t>(p.H) * 2u;
+      asm volatile("" : "+s"(ybase), "+s"(ystride));
+      constexpr int NR = 2 * MF;                                           // rounds of 8 rows
+      const int n_ok = t.row_end - t.row0 - wm * 64;                       // rows of this wave's 64 that exist
+      const int* const rmap = s_rows + parity * BM + wm * 64 + lrow;
+      u32x4 w[NF / 2], d[2];
+      int cell[2];                                                         // (token, slot) cells of the stores
 #pragma unroll
-      for (int i = 0; i < MF; ++i) {
-        u32x4 w[NF / 2];
+      for (int k = 0; k <= NR; ++k) {
+        if (k < NR) {
+          const int i = k >> 1, half = k & 1;
+          // packed again for each half (the VALU is otherwise idle here):
+          // holding the packed row fragment across both halves costs the
+          // registers that the read-back of the previous round needs (the
+          // empty asm keeps the compiler from reusing the first packing)
+          if (half == 1)
 #pragma unroll
-        for (int jp = 0; jp < NF / 2; ++jp)
+            for (int j = 0; j < NF; ++j) pin_acc(acc[i][j]);
 #pragma unroll
-          for (int h = 0; h < 4; ++h)
-            w[jp][h] = pack_bf16x2(acc[i][2 * jp + h / 2][2 * (h & 1)], acc[i][2 * jp + h / 2][2 * (h & 1) + 1]);
+          for (int jp = 0; jp < NF / 2; ++jp)
 #pragma unroll
-        for (int half = 0; half < 2; ++half) {
+            for (int h = 0; h < 4; ++h)
+              w[jp][h] = pack_bf16x2(acc[i][2 * jp + h / 2][2 * (h & 1)], acc[i][2 * jp + h / 2][2 * (h & 1) + 1]);
           if ((elr >> 3) == half) {
 #pragma unroll
             for (int jp = 0; jp < NF / 2; ++jp)
               *reinterpret_cast<u32x4*>(stg + (elr & 7) * 256 + (((4 * jp + elg) ^ (elr & 7)) << 4)) = w[jp];
           }
           asm volatile("" ::: "memory");
+        }
+        if (k > 0) {
+          const int kp = k - 1;
 #pragma unroll
           for (int sr = 0; sr < 2; ++sr) {
-            const int rr = 4 * sr + lrow;                                    // row of the slice
-            const u32x4 v = *reinterpret_cast<const u32x4*>(stg + rr * 256 + ((lchunk ^ rr) << 4));
-            const int r = wm * 64 + i * 16 + 8 * half + rr;
-            const int64_t row = s_rows[parity * BM + r];                     // (token, slot) cell
             // non-temporal: y (N*k rows, 268 MB at T=16384) is larger than
             // the MALL and read once by the combine (non-temporal loads as
             // well); kept out of it, it no longer evicts act, x and the
             // weights, which this and the next layer step read again
-            if (t.row0 + r < t.row_end)
-              __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(C + row * p.H + col0 + lchunk * 8));
+            if (8 * kp + 4 * sr + lrow < n_ok)
+              __builtin_nontemporal_store(
+                  d[sr], reinterpret_cast<__attribute__((address_space(1))) u32x4*>(
+                             ybase + static_cast<uint64_t>(static_cast<uint32_t>(cell[sr])) * ystride + lchunk * 16));
+          }
+          asm volatile("" ::: "memory");
+        }
+        if (k < NR) {
+#pragma unroll
+          for (int sr = 0; sr < 2; ++sr) {
+            const int rr = 4 * sr + lrow;                                  // row of the slice
+            d[sr] = *reinterpret_cast<const u32x4*>(stg + rr * 256 + ((lchunk ^ rr) << 4));
+            cell[sr] = rmap[8 * k + 4 * sr];
           }
           asm volatile("" ::: "memory");
         }
@@ -1274,9 +1303,9 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(MoeParams p) {
 // each wave two 16-column weight fragments (GEMM-1: 16 gate + the matching 16
 // up columns; GEMM-2: 32 output columns) against the chunk's two row
 // fragments.  There the time goes to streaming the weights from HBM, so each
-// wave keeps kSkinnyDepth K-steps of weight and row fragments in flight,
-// straight from global memory into VGPRs (no LDS, no barriers), and a
-// expert with no rows has no chunk, so its weights are never read.  K is walked in exactly
+// wave keeps DEPTH K-steps of weight and row fragments in flight, straight
+// from global memory into VGPRs (no barriers), and an expert with no rows has
+// no chunk, so its weights are never read.  K is walked in exactly
 // the main kernel's order (GEMM-2: its column tile's rotation of the K stages; the
 // same MFMA with the weight fragment as src0), so every output element gets
 // the same fp32 accumulation sequence and the same bits as from
@@ -1285,39 +1314,62 @@ namespace skinny {
 constexpr int NW = 4, NT = NW * 64;
 constexpr int MFC = 2;                        // row fragments per pass (32 rows)
 constexpr int DEPTH = 8;                      // K-steps of loads in flight
+// GEMM-2 of the fused launch: weight K-steps DEPTH .. DEPTH + LSTEPS - 1 of
+// each wave go to LDS before the wait (1 KiB per step and fragment: 64 KiB
+// per workgroup, so two workgroups fit on a CU)
+constexpr int LSTEPS = 8;
+// fused launch: GEMM-2's workgroups start streaming their weights once every
+// GEMM-1 workgroup of the chunk is this many blocks of DEPTH steps from the
+// end of its K loop
+constexpr int SIG_BLOCKS = 2;
+constexpr int LDS_W = NW * LSTEPS * 2 * 1024;
 // use this path when N * k is at most this (measured crossover against the
 // tiled kernel: GEMM-1 between 1024 and 2048 entries, GEMM-2 past 2048)
 constexpr int64_t kMaxEntries1 = 1024, kMaxEntries2 = 2048;
 static_assert(kMaxEntries1 == sched::kSmallRows, "schedule words of the small-batch launch");
 }  // namespace skinny
 
-// One workgroup's share of a small-batch GEMM: chunk `block / n_cb`, column
-// block `block % n_cb`.  FUSED (both GEMMs in one launch, GEMM-1's workgroups
-// first in the grid): GEMM-1 writes act with device-scope stores and, once
-// they are complete, adds one to its chunk's counter in `sched`; GEMM-2 loads
-// its first DEPTH steps of weights, then thread 0 waits (bounded) until the
-// chunk's counter shows every GEMM-1 column block, and only then are act's
-// rows loaded.  The workgroups are dispatched in grid order, so every GEMM-1
-// workgroup is resident before any GEMM-2 workgroup can wait, and every wait
-// ends.  The last GEMM-2 workgroup of a chunk to pass the wait returns its
-// two counters to zero.
+// One workgroup's share of a small-batch GEMM: a (chunk, column block) pair
+// (the mapping is below).  FUSED (both GEMMs in one launch, GEMM-1's
+// workgroups first in the grid): each GEMM-1 workgroup adds one to its
+// chunk's counter in `sched` twice, when it is SIG_BLOCKS blocks of DEPTH
+// steps from the end of its K loop (most of its weights are in) and when its
+// act stores (device scope) are complete.  A GEMM-2 workgroup reads its
+// destination cells, waits (thread 0, bounded) for the first count of every
+// GEMM-1 column block, then loads its first DEPTH weight steps into registers
+// and the next LSTEPS into LDS (`s_w`: each lane fetches exactly the 16 bytes
+// it later feeds the MFMA, so a step's fragment is read back at byte
+// 16 * lane of its 1 KiB block), waits for the second counts, and only then
+// loads act's rows.  GEMM-1's weights thus stream first, with the whole
+// memory bandwidth (measured on the 32-token decode layer: GEMM-1's K loops
+// end at 13.4 us instead of 16.3 us with both weight streams overlapping, the
+// launch takes 22.4-22.8 us instead of 25.9 us; counting at the last block
+// instead of two before the end: 23.5 us, three before: 23.3 us).  The
+// workgroups are dispatched in grid order, so every GEMM-1 workgroup is
+// resident before any GEMM-2 workgroup can wait, GEMM-1 never waits, and
+// every wait ends.  The last GEMM-2 workgroup of a chunk to pass the second
+// wait returns the chunk's two counters to zero.
 template <bool GEMM1, bool FUSED>
 __device__ __forceinline__ void skinny_body(const GemmParams& p, int block, int n_cb_other, int* sched,
-                                            int* s_pre, int* s_off) {
+                                            int* s_pre, int* s_off, unsigned char* s_w) {
   using namespace skinny;
   typedef uint16_t T;
   constexpr int CH = 16 * MFC;                                // rows per workgroup
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nl = p.n_local;
-  // chunk table: expert j owns ceil(rows_j / CH) chunks of CH rows; workgroup
-  // b takes chunk b / n_cb in column block b % n_cb (the grid is sized for
-  // the worst case; workgroups past the last chunk return)
+  // chunk table: expert j owns ceil(rows_j / CH) chunks of CH rows.  The
+  // grid (sized for the worst case, a multiple of 8 chunks; workgroups past
+  // the last chunk return) runs chunk q's column blocks on workgroups
+  // b == q (mod 8): workgroups are dispatched to the 8 XCDs round robin, so a
+  // chunk's A rows are fetched into one XCD's L2 and shared there by all its
+  // column blocks (and in the fused launch GEMM-2 finds act where GEMM-1 of
+  // the same chunk wrote it)
   for (int j = tid; j <= nl; j += NT) s_off[j] = p.offsets[j];
   __syncthreads();
   if (tid < 64) scan_units<CH>(s_off, s_pre, nl, 1);
   __syncthreads();
   const int n_cb = GEMM1 ? p.N / 64 : p.N / 128;             // column blocks per expert
-  const int q = block / n_cb, cb = block % n_cb;
+  const int q = (block >> 3) / n_cb * 8 + (block & 7), cb = (block >> 3) % n_cb;
   const int n_chunks = s_pre[nl];
   if (q >= n_chunks) return;
   int lo = 0, hi = nl - 1;                                    // largest j with s_pre[j] <= q
@@ -1362,29 +1414,74 @@ __device__ __forceinline__ void skinny_body(const GemmParams& p, int block, int 
       if (ks >= KT) ks -= KT;
       return static_cast<int64_t>(ks) * 32;
     };
+    // steps held in LDS (fused GEMM-2 only): [DEPTH, DEPTH + n_lds)
+    constexpr bool LDS_STEPS = FUSED && !GEMM1;
+    const int n_lds = LDS_STEPS ? min(LSTEPS, KT - DEPTH) : 0;
+    unsigned char* const w_lds = LDS_STEPS ? s_w + wave * (LSTEPS * 2 * 1024) : nullptr;
     auto load_w = [&](int t, int slot) {
+      if (LDS_STEPS && t >= DEPTH && t < DEPTH + n_lds) {
+        const unsigned char* b = w_lds + (t - DEPTH) * 2048 + 16 * lane;
+        wq[slot][0] = *reinterpret_cast<const u32x4*>(b);
+        wq[slot][1] = *reinterpret_cast<const u32x4*>(b + 1024);
+        return;
+      }
       const int64_t off = k_off(t);
       wq[slot][0] = *reinterpret_cast<const u32x4*>(wp0 + off);
       wq[slot][1] = *reinterpret_cast<const u32x4*>(wp1 + off);
     };
-    if constexpr (FUSED && !GEMM1) {
-      // the weights do not depend on GEMM-1: their first steps go out before the wait
+    if constexpr (!LDS_STEPS) {
+      // the weights need only the chunk's expert: their first steps go out
+      // before the row map is read
 #pragma unroll
       for (int d = 0; d < DEPTH; ++d) load_w(d, d);
-      if (tid == 0) {
-        int polls = 0;
-        while (atomic_read(done1) < n_cb_other) {
-          if (++polls == sched::kWaitLimit) {
-            atomic_or_1(sched + sched::kFlags, sched::kFlagWait);
-            break;
-          }
-          __builtin_amdgcn_s_sleep(2);
+    }
+    // GEMM-2's destination cells, read now rather than after the K loop
+    // (in the fused launch the read overlaps the wait for GEMM-1)
+    int cell[MFC];
+    if constexpr (!GEMM1) {
+#pragma unroll
+      for (int f = 0; f < MFC; ++f) cell[f] = p.perm[min(r0 + 16 * f + lr, row_hi - 1)];
+    }
+    // thread 0: until the chunk's counter reaches `target` (bounded; a
+    // give-up sets the wait flag and goes on)
+    auto wait_count = [&](int target) {
+      int polls = 0;
+      while (atomic_read(done1) < target) {
+        if (++polls == sched::kWaitLimit) {
+          atomic_or_1(sched + sched::kFlags, sched::kFlagWait);
+          break;
         }
+        __builtin_amdgcn_s_sleep(2);
+      }
+    };
+    if constexpr (LDS_STEPS) {
+      // GEMM-1 streams its weights first: every GEMM-1 workgroup of the
+      // chunk counts once when its last weight loads are out, so GEMM-2's
+      // weights do not take memory bandwidth from GEMM-1's until then (the
+      // chunk's act is ready at the second count)
+      if (tid == 0) wait_count(n_cb_other);
+      __syncthreads();
+      // the weights do not depend on GEMM-1's results: their first DEPTH
+      // steps go to registers and the next n_lds steps to LDS before the wait
+#pragma unroll
+      for (int d = 0; d < DEPTH; ++d) load_w(d, d);
+      const unsigned char* wb = reinterpret_cast<const unsigned char*>(W);
+      const int wbytes = static_cast<int>(p.w_expert_stride * 2);
+      const uint32_t lo0 = static_cast<uint32_t>((wp0 - W) * 2), lo1 = static_cast<uint32_t>((wp1 - W) * 2);
+      for (int t = DEPTH; t < DEPTH + n_lds; ++t) {
+        const uint32_t ko = static_cast<uint32_t>(k_off(t) * 2);
+        buffer_lds_16(wb, wbytes, lo0 + ko, 0, w_lds + (t - DEPTH) * 2048);
+        buffer_lds_16(wb, wbytes, lo1 + ko, 0, w_lds + (t - DEPTH) * 2048 + 1024);
+      }
+      if (tid == 0) {
+        wait_count(2 * n_cb_other);
         if (atomic_add_1(seen2, 1) == n_cb - 1) {
           atomicExch(done1, 0);
           atomicExch(seen2, 0);
         }
       }
+      // this wave's LDS steps have landed (its own lanes read them back)
+      __builtin_amdgcn_s_waitcnt(kVmcnt0);
       __syncthreads();
     }
     // A rows of the pass (rows past row_hi read the last row; never stored)
@@ -1410,11 +1507,12 @@ __device__ __forceinline__ void skinny_body(const GemmParams& p, int block, int 
 #pragma unroll
       for (int j = 0; j < 2; ++j) acc[f][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int d = 0; d < DEPTH; ++d) {
-      if constexpr (!(FUSED && !GEMM1)) load_w(d, d);
-      load_a(d, d);
-    }
+    for (int d = 0; d < DEPTH; ++d) load_a(d, d);
     for (int t0 = 0; t0 < KT; t0 += DEPTH) {             // KT is a multiple of DEPTH
+      // fused GEMM-1: the first count of the chunk, SIG_BLOCKS blocks of
+      // DEPTH steps before the end of the K loop (at its start when shorter)
+      if (FUSED && GEMM1 && t0 == (KT > SIG_BLOCKS * DEPTH ? KT - SIG_BLOCKS * DEPTH : 0) && tid == 0)
+        atomic_add_1(done1, 1);
 #pragma unroll
       for (int d = 0; d < DEPTH; ++d) {
 #pragma unroll
@@ -1451,7 +1549,7 @@ __device__ __forceinline__ void skinny_body(const GemmParams& p, int block, int 
         if constexpr (FUSED) __hip_atomic_store(dst, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         else *dst = v;
       } else {
-        const int64_t row = p.perm[r];                     // (token, slot) cell
+        const int64_t row = cell[f];                       // (token, slot) cell
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
           const int col = cb * 128 + wave * 32 + 16 * j + 4 * lg;
@@ -1473,7 +1571,7 @@ template <bool GEMM1>
 __global__ __launch_bounds__(skinny::NT) void moe_gemm_skinny_kernel(GemmParams p) {
   __shared__ int s_pre[bfk::NLMAX + 1];                       // chunks before expert j
   __shared__ int s_off[bfk::NLMAX + 1];
-  skinny_body<GEMM1, false>(p, blockIdx.x, 0, nullptr, s_pre, s_off);
+  skinny_body<GEMM1, false>(p, blockIdx.x, 0, nullptr, s_pre, s_off, nullptr);
 }
 
 // Both small-batch GEMMs in one launch: workgroups [0, g1_blocks) are GEMM-1's,
@@ -1482,16 +1580,25 @@ __global__ __launch_bounds__(skinny::NT) void moe_gemm_skinny_both_kernel(GemmPa
                                                                           int g1_blocks, int* sched) {
   __shared__ int s_pre[bfk::NLMAX + 1];
   __shared__ int s_off[bfk::NLMAX + 1];
+  __shared__ __attribute__((aligned(16))) unsigned char s_w[skinny::LDS_W];
   const int b = blockIdx.x;
-  if (b < g1_blocks) skinny_body<true, true>(p1, b, p2.N / 128, sched, s_pre, s_off);
-  else skinny_body<false, true>(p2, b - g1_blocks, p1.N / 64, sched, s_pre, s_off);
+  if (b < g1_blocks) skinny_body<true, true>(p1, b, p2.N / 128, sched, s_pre, s_off, s_w);
+  else skinny_body<false, true>(p2, b - g1_blocks, p1.N / 64, sched, s_pre, s_off, s_w);
+}
+
+// chunks of the small-batch grids: the worst case (each expert adds at most
+// one partial chunk), rounded up to a multiple of 8 (one per XCD, see
+// skinny_body), so GEMM-1's block count is a multiple of 8 as well
+inline int64_t skinny_chunks(int64_t max_rows, int n_local) {
+  const int64_t c = (max_rows + 16 * skinny::MFC - 1) / (16 * skinny::MFC) + n_local;
+  return (c + 7) / 8 * 8;
 }
 
 template <bool GEMM1>
 hipError_t launch_skinny(const GemmParams& p, int64_t max_rows, hipStream_t stream) {
   // few rows per expert: stream each expert's weights once (same results)
   const int n_cb = GEMM1 ? p.N / 64 : p.N / 128;
-  const int64_t chunks = (max_rows + 16 * skinny::MFC - 1) / (16 * skinny::MFC) + p.n_local;
+  const int64_t chunks = skinny_chunks(max_rows, p.n_local);
   const int64_t blocks = chunks * n_cb;
   if (blocks == 0) return hipSuccess;
   moe_gemm_skinny_kernel<GEMM1><<<dim3(static_cast<unsigned>(blocks)), skinny::NT, 0, stream>>>(p);
@@ -1500,7 +1607,7 @@ hipError_t launch_skinny(const GemmParams& p, int64_t max_rows, hipStream_t stre
 
 hipError_t launch_skinny_both(const GemmParams& p1, const GemmParams& p2, int64_t max_rows, int* sched,
                               hipStream_t stream) {
-  const int64_t chunks = (max_rows + 16 * skinny::MFC - 1) / (16 * skinny::MFC) + p1.n_local;
+  const int64_t chunks = skinny_chunks(max_rows, p1.n_local);
   const int64_t b1 = chunks * (p1.N / 64), b2 = chunks * (p2.N / 128);
   if (b1 + b2 == 0) return hipSuccess;
   moe_gemm_skinny_both_kernel<<<dim3(static_cast<unsigned>(b1 + b2)), skinny::NT, 0, stream>>>(

@@ -219,19 +219,24 @@ def test_one_launch_equals_two_launches(case):
         assert (to_np(y1)[np.repeat(~valid.numpy(), k)] == 7.0).all()
 
 
-@pytest.mark.parametrize("case", ["decode_t32", "zipf_t128", "masked_t100", "e64_t16"])
+@pytest.mark.parametrize("case", ["decode_t32", "zipf_t128", "masked_t100", "e64_t16", "h256_t32", "i1024_t24"])
 def test_small_batch_one_launch_equals_two_launches(case):
     """Batches of at most 1024 (token, slot) entries run both small-batch
-    GEMMs as one launch (GEMM-2's workgroups load their weights, then wait
-    for their chunk's GEMM-1 workgroups).  Bits equal the two launches on
-    every row, other rows are left alone, the schedule words return to zero,
-    and consecutive calls on other inputs (the same act workspace) give each
-    input's own result."""
+    GEMMs as one launch (GEMM-2's workgroups start loading their weights when
+    their chunk's GEMM-1 workgroups near the end of their K loops, then wait
+    for act).  Bits equal the two launches on every row, other rows are left
+    alone, the schedule words return to zero, no wait gives up, and
+    consecutive calls on other inputs (the same act workspace) give each
+    input's own result.  h256: GEMM-1's K loop is one block of loads in
+    flight (the early count at its start); i1024: GEMM-2 has weight steps
+    past those held in LDS."""
     banner(f"experts small-batch one launch vs two: {case}")
     bf = torch.bfloat16
     g = torch.Generator().manual_seed(21)
     E = 64 if case.startswith("e64") else 32
     n = int(case.split("_t")[1])
+    H = 256 if case.startswith("h256") else 1024
+    I = 256 if case.startswith("h256") else (1024 if case.startswith("i1024") else 512)
     valid = None
     if case.startswith("zipf"):
         L = workloads.make_layer(n, seed=21, zipf_s=1.2)
@@ -239,8 +244,8 @@ def test_small_batch_one_launch_equals_two_launches(case):
         x, w_in, w_out = L.x, L.w_in, L.w_out
     else:
         topk = torch.rand(n, E, generator=g).topk(8, -1).indices
-        x = torch.randn(n, 1024, generator=g)
-        w_in, w_out = workloads.expert_weights(g, E)
+        x = torch.randn(n, H, generator=g)
+        w_in, w_out = workloads.expert_weights(g, E, hidden=H, inter=I)
         if case.startswith("masked"):
             valid = torch.rand(n, generator=g) < 0.7
     k = 8
@@ -252,7 +257,7 @@ def test_small_batch_one_launch_equals_two_launches(case):
     results = []
     for rep in range(2):                                   # a second input through the same buffers
         xd = (x if rep == 0 else torch.randn(x.shape, generator=g)).to(bf).to(DEV)
-        y1 = torch.full((n * k, 1024), 7.0, dtype=bf, device=DEV)
+        y1 = torch.full((n * k, H), 7.0, dtype=bf, device=DEV)
         y2 = y1.clone()
         ops.grouped_swiglu(xd, d, wi, wo, y1)
         _two_launches(xd, d, wi, wo, y2)
