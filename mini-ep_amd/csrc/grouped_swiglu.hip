@@ -4,7 +4,7 @@
 // (modeling.py:143):
 //     for each local expert e:  h = X_e @ W_in[e].T ; gate, up = h.chunk(2)
 //                               y = (silu(gate) * up) @ W_out[e].T ; out[idx] = y
-// as two launches over the dispatched rows (grouped by expert, ragged):
+// over the dispatched rows (grouped by expert, ragged), as two GEMMs:
 //   GEMM-1  act[r, :] = silu(x[perm[r]/k] W_g^T) * (x[perm[r]/k] W_u^T)
 //           A rows are gathered from x inside the tile load (no permuted copy
 //           of x is ever written); every output tile holds matching gate and
@@ -27,16 +27,22 @@
 // 128-byte lines and stores them non-temporally (y_entries is read once, by
 // the combine).  fp32 keeps the simpler two-stage grouped_gemm_kernel.
 //
-// Scheduling (bf16): persistent, one workgroup per CU.  The tile list
-// (expert, m-tile, n-tile) is derived on the device from `offsets` (no host
-// round trip for the counts).  XCD x owns a contiguous run of tiles, and its
-// workgroups take them in whole rounds (the 4 column tiles of a row tile sit
-// on the same 4 slots of one XCD, so they share rows and weights in its L2);
-// the tiles left after the whole rounds form one pool that workgroups take
-// through an atomic counter in the caller's tile queue.  The next tile's first
-// two stages stream in during the last four steps and the epilogue of the
-// current one.  Within a step, a wave two MFMA groups in runs at raised
-// priority, which keeps the two waves of a SIMD from moving in lockstep.
+// Scheduling (bf16, more than 1024 rows): persistent, one workgroup per CU,
+// both GEMMs in one launch (kModeBoth; kModeGateUp / kModeDown run one of
+// them).  The row tiles, derived on the device from `offsets` (no host round
+// trip for the counts), are split into one contiguous range per XCD; each
+// XCD's workgroups take its GEMM-1 column tiles, then its GEMM-2 column tiles,
+// the first item of each workgroup fixed and the rest claimed one at a time
+// from the queue's counter in the caller's `tile_queue`, and take other
+// queues' items once their own is drained.  A GEMM-2 tile starts when every
+// GEMM-1 tile of its row tile has counted its act rows complete.  The next
+// tile's first two stages stream in during the last four steps and the
+// epilogue of the current one.  Within a step, a wave two MFMA groups in runs
+// at raised priority, which keeps the two waves of a SIMD from moving in
+// lockstep.  At most 1024 rows (decode, small batches) run the small-batch
+// kernels below instead: a workgroup per 32-row chunk and column block,
+// weights streamed straight into registers, both GEMMs in one launch.  Every
+// path walks K in the same order, so they give the same bits.
 #include "common.h"
 
 #include <type_traits>
@@ -444,8 +450,8 @@ hipError_t launch(const GemmParams& p, int64_t max_rows, hipStream_t stream) {
 // MFMAs run column-major (the 4 MFMAs of weight fragment j, then j+1): row
 // fragments are double-buffered, weight fragment j is refilled right after its
 // group.  The MFMAs are inline asm with "+v" accumulators: the 128
-// accumulators stay in arch VGPRs next to everything else (226-244 of the 256
-// a wave has at two waves per SIMD), so the epilogue reads them without 128
+// accumulators stay in arch VGPRs next to everything else (the kernel uses
+// all 256 a wave has at two waves per SIMD), so the epilogue reads them without 128
 // v_accvgpr_read moves (with the builtin the compiler moves them between
 // register files and spills).
 //
