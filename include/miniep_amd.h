@@ -17,6 +17,8 @@
  *                       SiLU*up, GEMM-2, scatter); also as
  *                       mep_swiglu_gate_up + mep_swiglu_down
  *   mep_combine         gate * y, slot-order sum           modeling.py:120-128,144
+ *   mep_grouped_swiglu_combine   the last two in one call (one launch for
+ *                       small bf16 top-8 batches)          modeling.py:98-104,120-128,144
  *
  * Conventions
  *  - Every pointer argument is DEVICE memory unless marked "host".
@@ -222,8 +224,9 @@ int mep_route_dispatch(const void* x, const void* w_router, const uint8_t* valid
  * keep their schedule there (per-XCD tile counters, per-row-tile or
  * per-chunk GEMM-1 completion counts) and every launch leaves it zero again,
  * except word 10: sticky error flags that mep_experts_check reports (a
- * GEMM-2 tile that gave up waiting for its rows after about a second, a
- * queue that no workgroup drained; either means the results are invalid).  Launches that may run at
+ * GEMM-2 tile that gave up waiting for its rows after about a second, or the
+ * combine of mep_grouped_swiglu_combine for GEMM-2's, a queue that no
+ * workgroup drained; either means the results are invalid).  Launches that may run at
  * the same time (on different streams) need different queues; launches on
  * one stream can share one.  No counterpart in the reference (its experts
  * are a Python loop).
@@ -280,6 +283,27 @@ int mep_grouped_swiglu_slots(const void* x, int64_t n_tokens, int32_t top_k,
                              const int32_t* w_slot, int32_t hidden, int32_t inter, int32_t dtype,
                              void* y_entries, void* workspace, size_t workspace_bytes,
                              int32_t* tile_queue, size_t tile_queue_ints, void* stream);
+
+/*
+ * mep_grouped_swiglu_combine: mep_grouped_swiglu followed by mep_combine, the
+ * expert half of LocalMoEBackend.__call__ (modeling.py:98-104 run_experts,
+ * :120-128 scatter_combine, :144 the gate multiply) in one call.  Arguments
+ * are those of the two calls; max_rows must be n_tokens * top_k (every
+ * (token, slot) cell of y_entries), out is (n_tokens, H) like mep_combine's.
+ * For bf16, top-8 and at most 1024 rows (decode) the small-batch launch of
+ * both GEMMs ends with the combine: extra workgroups wait (bounded) until
+ * every GEMM-2 workgroup's y stores are complete, then sum in slot order, so
+ * the results equal the two calls' bit for bit with one launch fewer.  Other
+ * sizes and dtypes make the two calls.  Schedule words 12 and 13 of
+ * `tile_queue` serve the combine and are left at zero.
+ */
+int mep_grouped_swiglu_combine(const void* x, int64_t n_tokens, int32_t top_k, const int32_t* perm,
+                               const int32_t* offsets, const int32_t* row_of_entry,
+                               const void* topk_gate, const uint8_t* valid_mask, int32_t n_local,
+                               int64_t max_rows, const void* w_in, const void* w_out, int32_t hidden,
+                               int32_t inter, int32_t dtype, void* y_entries, void* workspace,
+                               size_t workspace_bytes, int32_t* tile_queue, size_t tile_queue_ints,
+                               void* out, void* stream);
 
 int mep_copy_experts(const void* src_in, const void* src_out, int32_t n_src,
                      void* dst_in, void* dst_out, int32_t n_slots,

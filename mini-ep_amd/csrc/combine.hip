@@ -16,6 +16,7 @@
 // destination sort): mep_combine_rows.  Its send-buffer counterpart,
 // mep_gather_rows (ep.py:226, x_flat[token_ids[order]]), copies the rows of x
 // in send order.
+#include "combine_dev.h"
 #include "common.h"
 
 namespace mep {
@@ -49,23 +50,6 @@ __device__ __forceinline__ void accumulate_cell(float* acc, float g, const u32x4
     acc[2] += g * __uint_as_float(v.z);
     acc[3] += g * __uint_as_float(v.w);
   }
-}
-
-template <int DT>
-__device__ __forceinline__ u32x4 pack_row_chunk(const float* acc) {
-  u32x4 o;
-  if constexpr (DT == MEP_DTYPE_BF16) {
-    o.x = pack_bf16x2(acc[0], acc[1]);
-    o.y = pack_bf16x2(acc[2], acc[3]);
-    o.z = pack_bf16x2(acc[4], acc[5]);
-    o.w = pack_bf16x2(acc[6], acc[7]);
-  } else {
-    o.x = __float_as_uint(acc[0]);
-    o.y = __float_as_uint(acc[1]);
-    o.z = __float_as_uint(acc[2]);
-    o.w = __float_as_uint(acc[3]);
-  }
-  return o;
 }
 
 // Any k: the token's row_of_entry entries and gates are read by each of its
@@ -104,11 +88,8 @@ __global__ __launch_bounds__(kThreads) void combine_kernel(const typename Elem<D
   *reinterpret_cast<u32x4*>(out + t * hidden + c * EPC) = pack_row_chunk<DT>(acc);
 }
 
-// k = 8, (token, slot) layout: the 8 cells of a token, its row_of_entry
-// entries, gates and valid flag are independent loads, all issued together
-// (no LDS staging and no barrier before the first y load).  An absent cell is
-// skipped with a select, so whatever an unwritten cell holds never reaches the
-// sum, and the sum is the same slot-order sequence as in combine_kernel.
+// k = 8, (token, slot) layout: combine8_chunk (combine_dev.h), the same
+// slot-order sum as combine_kernel, with y read by non-temporal loads.
 template <int DT>
 __global__ __launch_bounds__(kThreads) void combine8_kernel(const typename Elem<DT>::T* __restrict__ y,
                                                             const typename Elem<DT>::T* __restrict__ gate,
@@ -117,53 +98,15 @@ __global__ __launch_bounds__(kThreads) void combine8_kernel(const typename Elem<
                                                             int64_t n_tokens, int hidden,
                                                             typename Elem<DT>::T* __restrict__ out) {
   typedef typename Elem<DT>::T T;
-  constexpr int K = 8;
   constexpr int EPC = 16 / Elem<DT>::kBytes;
   int64_t t;
   int c;
   if (!chunk_of_thread(n_tokens, hidden / EPC, t, c)) return;
-  const T* ybase = y + (t * K) * hidden + c * EPC;
-  u32x4 v[K];
   // y is read exactly once: non-temporal loads keep these 268 MB (T=16384)
   // from evicting x and the weights from the 256 MB MALL before the next layer
-#pragma unroll
-  for (int s = 0; s < K; ++s)
-    v[s] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(ybase + static_cast<int64_t>(s) * hidden));
-  int32_t row[K];
-  float g[K];
-#pragma unroll
-  for (int s = 0; s < K; ++s) {
-    row[s] = row_of_entry[t * K + s];
-    g[s] = Elem<DT>::to_f32(gate[t * K + s]);
-  }
-  const bool tok_ok = valid == nullptr || valid[t] != 0;
-  float acc[EPC];
-#pragma unroll
-  for (int q = 0; q < EPC; ++q) acc[q] = 0.0f;
-#pragma unroll
-  for (int s = 0; s < K; ++s) {
-    const bool here = tok_ok && row[s] >= 0;
-    float yv[EPC];
-    if constexpr (DT == MEP_DTYPE_BF16) {
-      const uint32_t w[4] = {v[s].x, v[s].y, v[s].z, v[s].w};
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        yv[2 * q] = bf16_to_f32(static_cast<uint16_t>(w[q] & 0xffffu));
-        yv[2 * q + 1] = bf16_to_f32(static_cast<uint16_t>(w[q] >> 16));
-      }
-    } else {
-      yv[0] = __uint_as_float(v[s].x);
-      yv[1] = __uint_as_float(v[s].y);
-      yv[2] = __uint_as_float(v[s].z);
-      yv[3] = __uint_as_float(v[s].w);
-    }
-#pragma unroll
-    for (int q = 0; q < EPC; ++q) {
-      const float sum = acc[q] + g[s] * yv[q];
-      acc[q] = here ? sum : acc[q];
-    }
-  }
-  *reinterpret_cast<u32x4*>(out + t * hidden + c * EPC) = pack_row_chunk<DT>(acc);
+  combine8_chunk<DT>(y, gate, row_of_entry, valid, t, c, hidden, out, [](const T* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  });
 }
 
 // out[i, :] = x[perm[i] / top_k, :] (and ids_out[i] = topk_flat[perm[i]]):

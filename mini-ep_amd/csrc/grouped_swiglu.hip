@@ -43,6 +43,7 @@
 // kernels below instead: a workgroup per 32-row chunk and column block,
 // weights streamed straight into registers, both GEMMs in one launch.  Every
 // path walks K in the same order, so they give the same bits.
+#include "combine_dev.h"
 #include "common.h"
 
 #include <type_traits>
@@ -497,12 +498,16 @@ static_assert(BPW == NF, "one DMA block per MFMA group of an odd step");
 //   9                items computed
 //   10               error flags, sticky (never cleared by a launch):
 //                    kFlagWait  a GEMM-2 tile gave up waiting for its rows
+//                               (or the combine for GEMM-2's)
 //                    kFlagDrain items computed != items listed (never expected)
 //   11               bit per drained queue
+//   12, 13           small-batch launch ending with the combine: GEMM-2
+//                    workgroups done, combine workgroups past their wait
 //   [16, 16 + RT)    GEMM-1 column tiles finished per row tile (kModeBoth)
 // Every launch leaves every word but 10 zero.
 namespace sched {
-constexpr int kQueue = 0, kDone = 8, kItems = 9, kFlags = 10, kDrained = 11, kRowDone = 16;
+constexpr int kQueue = 0, kDone = 8, kItems = 9, kFlags = 10, kDrained = 11, kG2Done = 12, kCombDone = 13,
+              kRowDone = 16;
 constexpr int kFlagWait = 1, kFlagDrain = 2;
 constexpr int kWaitLimit = 1 << 20;            // polls of one row counter (about a second)
 // the small-batch launch of both GEMMs runs up to this many rows
@@ -635,6 +640,20 @@ __device__ __forceinline__ void store_dev_16(void* base, uint32_t bytes, uint32_
   __builtin_amdgcn_raw_buffer_store_b128(
       v, __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(bs), 0,
                                            __builtin_amdgcn_readfirstlane(static_cast<int>(bytes)), bfk::kBufWord3),
+      voff, 0, 16 /* sc1: device scope */);
+}
+
+// 16-byte load with device scope (sc1): it does not return a line this XCD's
+// caches kept from before another XCD rewrote it.  base / bytes as in
+// buffer_lds_16.
+__device__ __forceinline__ u32x4 load_dev_16(const void* base, uint32_t bytes, uint32_t voff) {
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(b >> 32)));
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(b & 0xFFFFFFFFu)));
+  const uint64_t bs = (static_cast<uint64_t>(hi) << 32) | lo;
+  return __builtin_amdgcn_raw_buffer_load_b128(
+      __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(bs), 0,
+                                        __builtin_amdgcn_readfirstlane(static_cast<int>(bytes)), bfk::kBufWord3),
       voff, 0, 16 /* sc1: device scope */);
 }
 
@@ -1335,6 +1354,19 @@ constexpr int64_t kMaxEntries1 = 1024, kMaxEntries2 = 2048;
 static_assert(kMaxEntries1 == sched::kSmallRows, "schedule words of the small-batch launch");
 }  // namespace skinny
 
+// The combine that ends a small-batch launch (moe_gemm_skinny_both_kernel
+// with COMB): top-8, bf16, the (token, slot) layout of y_entries.
+struct CombineParams {
+  const uint16_t* gate;            // (n_tokens, 8)
+  const int32_t* row_of_entry;     // (n_tokens * 8), -1: cell not computed
+  const uint8_t* valid;            // (n_tokens,) or NULL
+  uint16_t* out;                   // (n_tokens, hidden)
+  int64_t n_tokens;
+  int hidden;
+  int n_g2, n_comb;                // GEMM-2 and combine workgroups of the launch
+  uint32_t y_bytes;                // bytes of y_entries (< 4 GiB)
+};
+
 // One workgroup's share of a small-batch GEMM: a (chunk, column block) pair
 // (the mapping is below).  FUSED (both GEMMs in one launch, GEMM-1's
 // workgroups first in the grid): each GEMM-1 workgroup adds one to its
@@ -1355,9 +1387,13 @@ static_assert(kMaxEntries1 == sched::kSmallRows, "schedule words of the small-ba
 // resident before any GEMM-2 workgroup can wait, GEMM-1 never waits, and
 // every wait ends.  The last GEMM-2 workgroup of a chunk to pass the second
 // wait returns the chunk's two counters to zero.
-template <bool GEMM1, bool FUSED>
+// COMB (GEMM-2 of a launch that ends with the combine): y is stored with
+// device scope, and every GEMM-2 workgroup, with rows or without, counts
+// itself done in `sched` once its stores are complete.
+template <bool GEMM1, bool FUSED, bool COMB = false>
 __device__ __forceinline__ void skinny_body(const GemmParams& p, int block, int n_cb_other, int* sched,
                                             int* s_pre, int* s_off, unsigned char* s_w) {
+  static_assert(!COMB || (FUSED && !GEMM1), "the combine follows the fused launch's GEMM-2");
   using namespace skinny;
   typedef uint16_t T;
   constexpr int CH = 16 * MFC;                                // rows per workgroup
@@ -1377,7 +1413,10 @@ __device__ __forceinline__ void skinny_body(const GemmParams& p, int block, int 
   const int n_cb = GEMM1 ? p.N / 64 : p.N / 128;             // column blocks per expert
   const int q = (block >> 3) / n_cb * 8 + (block & 7), cb = (block >> 3) % n_cb;
   const int n_chunks = s_pre[nl];
-  if (q >= n_chunks) return;
+  if (q >= n_chunks) {
+    if (COMB && tid == 0) atomic_add_1(sched + sched::kG2Done, 1);
+    return;
+  }
   int lo = 0, hi = nl - 1;                                    // largest j with s_pre[j] <= q
   while (lo < hi) {
     const int mid = (lo + hi + 1) >> 1;
@@ -1560,7 +1599,11 @@ __device__ __forceinline__ void skinny_body(const GemmParams& p, int block, int 
         for (int j = 0; j < 2; ++j) {
           const int col = cb * 128 + wave * 32 + 16 * j + 4 * lg;
           const uint2 w = make_uint2(pack_bf16x2(acc[f][j][0], acc[f][j][1]), pack_bf16x2(acc[f][j][2], acc[f][j][3]));
-          *reinterpret_cast<uint2*>(C + row * p.N + col) = w;
+          if constexpr (COMB)   // device scope: the combine may run on another XCD
+            __hip_atomic_store(reinterpret_cast<uint64_t*>(C + row * p.N + col),
+                               (static_cast<uint64_t>(w.y) << 32) | w.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          else
+            *reinterpret_cast<uint2*>(C + row * p.N + col) = w;
         }
       }
     }
@@ -1571,6 +1614,46 @@ __device__ __forceinline__ void skinny_body(const GemmParams& p, int block, int 
     __syncthreads();
     if (tid == 0) atomic_add_1(done1, 1);
   }
+  if constexpr (COMB) {
+    // every wave's y stores are complete before the count goes up
+    __builtin_amdgcn_s_waitcnt(kVmcnt0);
+    __syncthreads();
+    if (tid == 0) atomic_add_1(sched + sched::kG2Done, 1);
+  }
+}
+
+// Combine workgroup `cb` of a launch that ends with the combine: thread 0
+// waits (bounded) until every GEMM-2 workgroup has counted its y stores
+// complete; the last combine workgroup past the wait returns both counters
+// to zero.  Then each thread sums one 16-byte chunk of a token's output row
+// (combine8_chunk: the order of combine8_kernel, so the same bits), reading y
+// with device-scope loads.
+__device__ void skinny_combine(const CombineParams& cp, const uint16_t* y, int cb, int* sched) {
+  const int tid = threadIdx.x;
+  if (tid == 0) {
+    int polls = 0;
+    while (atomic_read(sched + sched::kG2Done) < cp.n_g2) {
+      if (++polls == sched::kWaitLimit) {
+        atomic_or_1(sched + sched::kFlags, sched::kFlagWait);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+    }
+    if (atomic_add_1(sched + sched::kCombDone, 1) == cp.n_comb - 1) {
+      atomicExch(sched + sched::kG2Done, 0);
+      atomicExch(sched + sched::kCombDone, 0);
+    }
+  }
+  __syncthreads();
+  const int cpr = cp.hidden / 8;                              // 16-byte chunks per row
+  const uint32_t q = static_cast<uint32_t>(cb) * skinny::NT + tid;
+  const int64_t t = q / static_cast<uint32_t>(cpr);
+  const int c = static_cast<int>(q - static_cast<uint32_t>(t) * cpr);
+  if (t >= cp.n_tokens) return;
+  combine8_chunk<MEP_DTYPE_BF16>(y, cp.gate, cp.row_of_entry, cp.valid, t, c, cp.hidden, cp.out,
+                                 [&](const uint16_t* ptr) {
+                                   return load_dev_16(y, cp.y_bytes, static_cast<uint32_t>((ptr - y) * 2));
+                                 });
 }
 
 template <bool GEMM1>
@@ -1581,15 +1664,21 @@ __global__ __launch_bounds__(skinny::NT) void moe_gemm_skinny_kernel(GemmParams 
 }
 
 // Both small-batch GEMMs in one launch: workgroups [0, g1_blocks) are GEMM-1's,
-// the rest GEMM-2's (see skinny_body).
+// the rest GEMM-2's (see skinny_body); with COMB the last cp.n_comb
+// workgroups then combine the tokens' rows (skinny_combine).  Workgroups are
+// dispatched in grid order, so every workgroup a combine workgroup waits for
+// is resident or done before it is.
+template <bool COMB>
 __global__ __launch_bounds__(skinny::NT) void moe_gemm_skinny_both_kernel(GemmParams p1, GemmParams p2,
-                                                                          int g1_blocks, int* sched) {
+                                                                          int g1_blocks, int* sched,
+                                                                          CombineParams cp) {
   __shared__ int s_pre[bfk::NLMAX + 1];
   __shared__ int s_off[bfk::NLMAX + 1];
   __shared__ __attribute__((aligned(16))) unsigned char s_w[skinny::LDS_W];
   const int b = blockIdx.x;
   if (b < g1_blocks) skinny_body<true, true>(p1, b, p2.N / 128, sched, s_pre, s_off, s_w);
-  else skinny_body<false, true>(p2, b - g1_blocks, p1.N / 64, sched, s_pre, s_off, s_w);
+  else if (!COMB || b < g1_blocks + cp.n_g2) skinny_body<false, true, COMB>(p2, b - g1_blocks, p1.N / 64, sched, s_pre, s_off, s_w);
+  else skinny_combine(cp, static_cast<const uint16_t*>(p2.C), b - g1_blocks - cp.n_g2, sched);
 }
 
 // chunks of the small-batch grids: the worst case (each expert adds at most
@@ -1611,13 +1700,22 @@ hipError_t launch_skinny(const GemmParams& p, int64_t max_rows, hipStream_t stre
   return hipGetLastError();
 }
 
+// comb: NULL, or the combine that ends the launch (its n_g2 / n_comb are set here)
 hipError_t launch_skinny_both(const GemmParams& p1, const GemmParams& p2, int64_t max_rows, int* sched,
-                              hipStream_t stream) {
+                              const CombineParams* comb, hipStream_t stream) {
   const int64_t chunks = skinny_chunks(max_rows, p1.n_local);
   const int64_t b1 = chunks * (p1.N / 64), b2 = chunks * (p2.N / 128);
   if (b1 + b2 == 0) return hipSuccess;
-  moe_gemm_skinny_both_kernel<<<dim3(static_cast<unsigned>(b1 + b2)), skinny::NT, 0, stream>>>(
-      p1, p2, static_cast<int>(b1), sched);
+  if (comb == nullptr) {
+    moe_gemm_skinny_both_kernel<false><<<dim3(static_cast<unsigned>(b1 + b2)), skinny::NT, 0, stream>>>(
+        p1, p2, static_cast<int>(b1), sched, CombineParams{});
+  } else {
+    CombineParams cp = *comb;
+    cp.n_g2 = static_cast<int>(b2);
+    cp.n_comb = static_cast<int>((cp.n_tokens * (cp.hidden / 8) + skinny::NT - 1) / skinny::NT);
+    moe_gemm_skinny_both_kernel<true><<<dim3(static_cast<unsigned>(b1 + b2 + cp.n_comb)), skinny::NT, 0, stream>>>(
+        p1, p2, static_cast<int>(b1), sched, cp);
+  }
   return hipGetLastError();
 }
 
@@ -1829,11 +1927,14 @@ int down_impl(const char* fn, const void* act, int64_t n_tokens, int32_t top_k, 
 
 // Both GEMMs: one launch of the tiled kernel when both would run tiled, else
 // the two launches.
+// comb: NULL, or a combine that the small-batch launch may end with; then
+// *combined tells whether it did (otherwise the caller runs the combine).
 int grouped_impl(const char* fn, const void* x, int64_t n_tokens, int32_t top_k, const int32_t* perm,
                  const int32_t* offsets, int32_t n_local, int64_t max_rows, const void* w_in, const void* w_out,
                  const int32_t* w_slot, int32_t hidden, int32_t inter, int32_t dtype, void* y_entries,
                  void* workspace, size_t workspace_bytes, int32_t* tile_queue, size_t tile_queue_ints,
-                 void* stream) {
+                 void* stream, const CombineParams* comb = nullptr, bool* combined = nullptr) {
+  if (combined != nullptr) *combined = false;
   int rc = check_expert_args(fn, n_tokens, top_k, n_local, max_rows, hidden, inter, dtype);
   if (rc != MEP_OK) return rc;
   if (max_rows == 0 || n_local == 0) return MEP_OK;
@@ -1865,8 +1966,9 @@ int grouped_impl(const char* fn, const void* x, int64_t n_tokens, int32_t top_k,
                                                                 w_slot, hidden, inter, workspace);
     const GemmParams g2 = gemm2_params<MEP_DTYPE_BF16, CfgBf16>(workspace, top_k, perm, offsets, n_local, max_rows,
                                                                 w_out, w_slot, hidden, inter, y_entries);
-    const hipError_t e = launch_skinny_both(g1, g2, max_rows, tile_queue, static_cast<hipStream_t>(stream));
+    const hipError_t e = launch_skinny_both(g1, g2, max_rows, tile_queue, comb, static_cast<hipStream_t>(stream));
     MEP_REQUIRE(e == hipSuccess, MEP_ERR_HIP, "%s: %s", fn, hipGetErrorString(e));
+    if (combined != nullptr) *combined = comb != nullptr;
     return MEP_OK;
   }
   rc = gate_up_impl(fn, x, n_tokens, top_k, perm, offsets, n_local, max_rows, w_in, w_slot, hidden, inter, dtype,
@@ -1893,7 +1995,8 @@ extern "C" int mep_experts_check(const int32_t* tile_queue, void* stream) {
   e = hipMemcpy(&flags, tile_queue + mep::sched::kFlags, sizeof(flags), hipMemcpyDeviceToHost);
   MEP_REQUIRE(e == hipSuccess, MEP_ERR_HIP, "mep_experts_check: %s", hipGetErrorString(e));
   MEP_REQUIRE(!(flags & mep::sched::kFlagWait), MEP_ERR_HIP,
-              "mep_experts_check: a GEMM-2 tile gave up waiting for its GEMM-1 rows (results invalid)");
+              "mep_experts_check: a workgroup gave up waiting (GEMM-2 for its GEMM-1 rows, or the combine for "
+              "GEMM-2's rows; results invalid)");
   MEP_REQUIRE(!(flags & mep::sched::kFlagDrain), MEP_ERR_HIP,
               "mep_experts_check: a tile queue was not drained (results invalid)");
   return MEP_OK;
@@ -1948,4 +2051,40 @@ extern "C" int mep_grouped_swiglu_slots(const void* x, int64_t n_tokens, int32_t
   return grouped_impl("mep_grouped_swiglu_slots", x, n_tokens, top_k, perm, offsets, n_local, max_rows, w_in,
                       w_out, w_slot, hidden, inter, dtype, y_entries, workspace, workspace_bytes, tile_queue,
                       tile_queue_ints, stream);
+}
+
+extern "C" int mep_grouped_swiglu_combine(const void* x, int64_t n_tokens, int32_t top_k, const int32_t* perm,
+                                          const int32_t* offsets, const int32_t* row_of_entry,
+                                          const void* topk_gate, const uint8_t* valid_mask, int32_t n_local,
+                                          int64_t max_rows, const void* w_in, const void* w_out, int32_t hidden,
+                                          int32_t inter, int32_t dtype, void* y_entries, void* workspace,
+                                          size_t workspace_bytes, int32_t* tile_queue, size_t tile_queue_ints,
+                                          void* out, void* stream) {
+  clear_error();
+  const char* fn = "mep_grouped_swiglu_combine";
+  MEP_REQUIRE(max_rows == n_tokens * static_cast<int64_t>(top_k), MEP_ERR_INVALID_ARG,
+              "%s: max_rows %lld must be n_tokens * top_k (every (token, slot) cell)", fn,
+              static_cast<long long>(max_rows));
+  MEP_REQUIRE(n_tokens == 0 || (row_of_entry && topk_gate && out), MEP_ERR_INVALID_ARG,
+              "%s: null row_of_entry / topk_gate / out", fn);
+  // the small-batch launch ends with the combine for bf16 top-8 (the other
+  // sizes run the experts and mep_combine as two launches, same results)
+  CombineParams cp{};
+  const bool fuse = dtype == MEP_DTYPE_BF16 && top_k == 8 && n_tokens > 0 && aligned16(out) &&
+                    aligned16(y_entries) && max_rows * hidden * 2 < (int64_t(1) << 32);
+  if (fuse) {
+    cp.gate = static_cast<const uint16_t*>(topk_gate);
+    cp.row_of_entry = row_of_entry;
+    cp.valid = valid_mask;
+    cp.out = static_cast<uint16_t*>(out);
+    cp.n_tokens = n_tokens;
+    cp.hidden = hidden;
+    cp.y_bytes = static_cast<uint32_t>(max_rows * hidden * 2);
+  }
+  bool combined = false;
+  int rc = grouped_impl(fn, x, n_tokens, top_k, perm, offsets, n_local, max_rows, w_in, w_out, nullptr, hidden,
+                        inter, dtype, y_entries, workspace, workspace_bytes, tile_queue, tile_queue_ints, stream,
+                        fuse ? &cp : nullptr, &combined);
+  if (rc != MEP_OK || combined) return rc;
+  return mep_combine(y_entries, topk_gate, row_of_entry, valid_mask, n_tokens, top_k, hidden, dtype, out, stream);
 }

@@ -82,6 +82,10 @@ _SIGNATURES = {
     "mep_grouped_swiglu_slots": (ctypes.c_int, [_c_void_p, _i64, _i32, _c_void_p, _c_void_p, _i32,
                                                 _i64, _c_void_p, _c_void_p, _c_void_p, _i32, _i32, _i32,
                                                 _c_void_p, _c_void_p, _size, _c_void_p, _size, _c_void_p]),
+    "mep_grouped_swiglu_combine": (ctypes.c_int, [_c_void_p, _i64, _i32, _c_void_p, _c_void_p, _c_void_p,
+                                                  _c_void_p, _c_void_p, _i32, _i64, _c_void_p, _c_void_p, _i32,
+                                                  _i32, _i32, _c_void_p, _c_void_p, _size, _c_void_p, _size,
+                                                  _c_void_p, _c_void_p]),
     "mep_copy_experts": (ctypes.c_int, [_c_void_p, _c_void_p, _i32, _c_void_p, _c_void_p, _i32,
                                         ctypes.POINTER(_i32), ctypes.POINTER(_i32), _i32, _i32, _i32, _i32,
                                         _c_void_p]),

@@ -59,8 +59,8 @@ class HipMoEBackend:
         disp = ops.dispatch(topk_idx, valid_mask, self.num_experts, self._table, self._n_rep,
                             False, None, 0, self._g2l, self.num_experts, check=self.check)
         self.last_dispatch = disp
-        y = ops.grouped_swiglu(x_flat.to(self.w_in.dtype), disp, self.w_in, self.w_out)
-        return ops.combine(y, topk_gate, disp.row_of_entry, valid_mask)
+        return ops.grouped_swiglu_combine(x_flat.to(self.w_in.dtype), disp, self.w_in, self.w_out, topk_gate,
+                                          valid_mask)
 
     def route_and_call(self, x_flat, w_router, k, valid_mask=None):
         """The router hook and this backend in one go (Block.forward,
@@ -70,8 +70,7 @@ class HipMoEBackend:
         x = x_flat.to(self.w_in.dtype)
         idx, gate, disp = ops.route_dispatch(x, w_router, k, valid_mask, check=self.check)
         self.last_dispatch = disp
-        y = ops.grouped_swiglu(x, disp, self.w_in, self.w_out)
-        return ops.combine(y, gate, disp.row_of_entry, valid_mask), idx, gate
+        return ops.grouped_swiglu_combine(x, disp, self.w_in, self.w_out, gate, valid_mask), idx, gate
 
 
 class EPStats:

@@ -301,6 +301,48 @@ def grouped_swiglu(x_flat: torch.Tensor, disp: Dispatch, w_in: torch.Tensor, w_o
     return y_entries
 
 
+def grouped_swiglu_combine(x_flat: torch.Tensor, disp: Dispatch, w_in: torch.Tensor, w_out: torch.Tensor,
+                           topk_gate: torch.Tensor, valid_mask: torch.Tensor | None = None,
+                           y_entries: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """grouped_swiglu followed by combine (mep_grouped_swiglu_combine): the
+    (n, H) layer output, the same bits as the two calls; for small bf16 top-8
+    batches the experts' launch ends with the combine (one launch fewer).
+    The dispatch must cover every (token, slot) cell (world 1)."""
+    dev = _require_device(x_flat, w_in, w_out, topk_gate, y_entries, out)
+    x = x_flat.contiguous()
+    n, h = x.shape
+    if w_in.dim() != 3 or w_out.dim() != 3:
+        raise ValueError("w_in must be (E, 2I, H) and w_out (E, H, I)")
+    e_loc, two_i, h_in = w_in.shape
+    inter = two_i // 2
+    if h_in != h or tuple(w_out.shape) != (e_loc, h, inter) or e_loc != disp.n_local:
+        raise ValueError(f"weight shapes {tuple(w_in.shape)} / {tuple(w_out.shape)} do not match "
+                         f"hidden {h} and {disp.n_local} local experts")
+    if tuple(topk_gate.shape) != (n, disp.top_k):
+        raise ValueError(f"topk_gate {tuple(topk_gate.shape)} does not match {n} tokens x top-{disp.top_k}")
+    wi = w_in.to(x.dtype).contiguous()
+    wo = w_out.to(x.dtype).contiguous()
+    gate = topk_gate.to(x.dtype).contiguous()
+    vm = _mask_u8(valid_mask, n)
+    max_rows = n * disp.top_k
+    if y_entries is None:
+        y_entries = torch.empty((max(max_rows, 1), h), dtype=x.dtype, device=dev)
+    if out is None:
+        out = torch.empty((n, h), dtype=x.dtype, device=dev)
+    code = _dtype_code(x)
+    L = _lib.lib()
+    ws_bytes = L.mep_experts_workspace_size(max_rows, inter, code)
+    ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
+    tq = _tile_queue(dev, max_rows, disp.n_local)
+    rc = L.mep_grouped_swiglu_combine(x.data_ptr(), n, disp.top_k, disp.perm.data_ptr(), disp.offsets.data_ptr(),
+                                      disp.row_of_entry.data_ptr(), gate.data_ptr(), _ptr(vm), disp.n_local,
+                                      max_rows, wi.data_ptr(), wo.data_ptr(), h, inter, code,
+                                      y_entries.data_ptr(), ws.data_ptr(), ws.numel(), tq.data_ptr(), tq.numel(),
+                                      out.data_ptr(), _stream(dev))
+    _lib.check(rc, "mep_grouped_swiglu_combine")
+    return out
+
+
 def copy_experts(src_in: torch.Tensor, src_out: torch.Tensor, src_index: list[int], dst_in: torch.Tensor,
                  dst_out: torch.Tensor, dst_slot: list[int]) -> None:
     """Slot dst_slot[i] of (dst_in, dst_out) = expert src_index[i] of

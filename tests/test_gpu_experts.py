@@ -334,3 +334,50 @@ def test_other_shapes_vs_oracle(H, I, E, k, n, dtype):
     err = rel_err(to_np(y), ref)
     print(f"rel err {err:.3e}")
     assert err <= (TOL_BF16 if bf else TOL_F32)
+
+
+@pytest.mark.parametrize("case", ["decode_t32", "masked_t100", "zipf_t128", "e64_t16", "h256_t32",
+                                  "bf16_t3000", "f32_t32"])
+def test_grouped_swiglu_combine_equals_two_calls(case):
+    """mep_grouped_swiglu_combine: for small bf16 top-8 batches the
+    small-batch launch ends with the combine (workgroups that wait for every
+    GEMM-2 workgroup's y stores, then sum in combine8's order); other sizes
+    and fp32 make the two calls.  The layer output equals grouped_swiglu +
+    combine bit for bit, masked tokens included, on two inputs in a row
+    through the same buffers, and the schedule words return to zero."""
+    banner(f"experts + combine in one call vs two: {case}")
+    dt = torch.float32 if case.startswith("f32") else torch.bfloat16
+    g = torch.Generator().manual_seed(33)
+    E = 64 if case.startswith("e64") else 32
+    n = int(case.split("_t")[1])
+    H = 256 if case.startswith("h256") else 1024
+    I = 256 if case.startswith("h256") else 512
+    valid = (torch.rand(n, generator=g) < 0.7) if case.startswith("masked") else None
+    if case.startswith("zipf"):
+        L = workloads.make_layer(n, seed=33, zipf_s=1.2)
+        logits = L.x @ L.w_router.T
+        x, w_in, w_out = L.x, L.w_in, L.w_out
+    else:
+        logits = torch.randn(n, E, generator=g)
+        x = torch.randn(n, H, generator=g)
+        w_in, w_out = workloads.expert_weights(g, E, hidden=H, inter=I)
+    top = torch.softmax(logits, -1).topk(8, -1)
+    topk, gate = top.indices, top.values
+    table, n_rep, g2l = _world1(E)
+    d = ops.dispatch(topk.to(DEV), None if valid is None else valid.to(DEV), E, table, n_rep, False, None, 0, g2l, E)
+    wi, wo = w_in.to(dt).to(DEV), w_out.to(dt).to(DEV)
+    gd = gate.to(dt).to(DEV)
+    vd = None if valid is None else valid.to(DEV)
+    outs = []
+    for rep in range(2):
+        xd = (x if rep == 0 else torch.randn(x.shape, generator=g)).to(dt).to(DEV)
+        ref = ops.combine(ops.grouped_swiglu(xd, d, wi, wo), gd, d.row_of_entry, vd)
+        got = ops.grouped_swiglu_combine(xd, d, wi, wo, gd, vd)
+        ops.experts_check()
+        assert torch.equal(got, ref), rep
+        for q in ops._QUEUES.values():
+            assert int(q.abs().sum()) == 0
+        if valid is not None:
+            assert (to_np(got)[~valid.numpy()] == 0).all()
+        outs.append(got)
+    assert not torch.equal(outs[0], outs[1])
