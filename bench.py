@@ -165,8 +165,9 @@ def mfma_busy_from_profile() -> dict | None:
 def decode_detail(dev, calls: int = 200) -> dict:
     """The decode-shaped layer (32 tokens, bf16, unbiased router: near-uniform
     load, most experts with 0-16 entries), HBM-bound on streaming the expert
-    weights of the experts it touches.  One call = route + dispatch, GEMM-1,
-    GEMM-2, combine (HipMoEBackend.route_and_call, 4 launches).  At this size
+    weights of the experts it touches.  One call = route + dispatch (one
+    launch), then GEMM-1, GEMM-2 and the combine (one launch)
+    (HipMoEBackend.route_and_call, 2 launches).  At this size
     the host's enqueue time is close to the GPU time, so the call is also
     captured in a HIP graph and replayed (a decode loop could replay it the
     same way); every replay is checked against the eager output.  HIP events
@@ -228,7 +229,7 @@ def decode_detail(dev, calls: int = 200) -> dict:
             "us_per_call": 1e3 * best, "us_per_call_eager": 1e3 * eager_ms, "us_per_call_graph": 1e3 * ms,
             "replays_equal_eager": replays_equal, "bytes": nbytes, "GB/s": nbytes / (best / 1e3) / 1e9,
             "frac_hbm": nbytes / (best / 1e3) / PEAK_HBM_BYTES, "floor_us": 1e6 * nbytes / PEAK_HBM_BYTES,
-            "measures": f"route_and_call (4 launches), {calls} calls back to back, HIP events, launched from Python "
+            "measures": f"route_and_call (2 launches), {calls} calls back to back, HIP events, launched from Python "
                         "(eager) and replayed from a HIP graph (graph); us_per_call is the faster of the two"}
 
 
