@@ -381,3 +381,40 @@ def test_grouped_swiglu_combine_equals_two_calls(case):
             assert (to_np(got)[~valid.numpy()] == 0).all()
         outs.append(got)
     assert not torch.equal(outs[0], outs[1])
+
+
+def test_decode_layer_graph_replay():
+    """HipMoEBackend.route_and_call at decode size (router + dispatch, then
+    the small-batch experts launch that ends with the combine) captured in a
+    HIP graph: every replay equals the eager call on the same input, with
+    eager calls on other inputs in between, and the schedule words the
+    launch's last workgroups return to zero stay zero."""
+    banner("decode layer graph replay")
+    from miniep_amd import HipMoEBackend
+    bf = torch.bfloat16
+    g = torch.Generator().manual_seed(44)
+    L = workloads.make_layer(32, seed=44)
+    be = HipMoEBackend(L.w_in.to(bf).to(DEV), L.w_out.to(bf).to(DEV), check=False)
+    w_r = L.w_router.to(bf).to(DEV)
+    xs = [torch.randn(32, 1024, generator=g).to(bf).to(DEV) for _ in range(2)]
+    x = xs[0].clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        be.route_and_call(x, w_r, 8)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            out = be.route_and_call(x, w_r, 8)[0]
+    torch.cuda.current_stream().wait_stream(side)
+    for rep in range(4):
+        x.copy_(xs[rep % 2])
+        want = be.route_and_call(x, w_r, 8)[0].clone()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), rep
+        be.route_and_call(xs[(rep + 1) % 2], w_r, 8)     # eager work on another input between replays
+        torch.cuda.synchronize()
+    ops.experts_check()
+    for q in ops._QUEUES.values():
+        assert int(q.abs().sum()) == 0
