@@ -1373,12 +1373,15 @@ struct CombineParams {
 // chunk's counter in `sched` twice, when it is SIG_BLOCKS blocks of DEPTH
 // steps from the end of its K loop (most of its weights are in) and when its
 // act stores (device scope) are complete.  A GEMM-2 workgroup reads its
-// destination cells, waits (thread 0, bounded) for the first count of every
-// GEMM-1 column block, then loads its first DEPTH weight steps into registers
-// and the next LSTEPS into LDS (`s_w`: each lane fetches exactly the 16 bytes
-// it later feeds the MFMA, so a step's fragment is read back at byte
-// 16 * lane of its 1 KiB block), waits for the second counts, and only then
-// loads act's rows.  GEMM-1's weights thus stream first, with the whole
+// destination cells, waits (thread 0, bounded) until the chunk's count
+// reaches the number of GEMM-1 column blocks (normally their first counts; a
+// mix of first and second counts meets it too, harmlessly: this wait only
+// orders the weight streams), then loads its first DEPTH weight steps into
+// registers and the next LSTEPS into LDS (`s_w`: each lane fetches exactly
+// the 16 bytes it later feeds the MFMA, so a step's fragment is read back at
+// byte 16 * lane of its 1 KiB block), waits until the count is twice the
+// column blocks (each adds exactly two, so every act store of the chunk is
+// complete), and only then loads act's rows.  GEMM-1's weights thus stream first, with the whole
 // memory bandwidth (measured on the 32-token decode layer: GEMM-1's K loops
 // end at 13.4 us instead of 16.3 us with both weight streams overlapping, the
 // launch takes 22.4-22.8 us instead of 25.9 us; counting at the last block
@@ -1501,9 +1504,9 @@ __device__ __forceinline__ void skinny_body(const GemmParams& p, int block, int 
     };
     if constexpr (LDS_STEPS) {
       // GEMM-1 streams its weights first: every GEMM-1 workgroup of the
-      // chunk counts once when its last weight loads are out, so GEMM-2's
-      // weights do not take memory bandwidth from GEMM-1's until then (the
-      // chunk's act is ready at the second count)
+      // chunk counts once SIG_BLOCKS blocks before the end of its K loop, so
+      // GEMM-2's weights do not take memory bandwidth from GEMM-1's until
+      // then (the chunk's act is ready when the count is twice the blocks)
       if (tid == 0) wait_count(n_cb_other);
       __syncthreads();
       // the weights do not depend on GEMM-1's results: their first DEPTH
