@@ -64,7 +64,6 @@ __global__ __launch_bounds__(kThreads) void combine_kernel(const typename Elem<D
                                                            const uint8_t* __restrict__ valid,
                                                            int64_t n_tokens, int k, int hidden,
                                                            typename Elem<DT>::T* __restrict__ out) {
-  typedef typename Elem<DT>::T T;
   constexpr int EPC = 16 / Elem<DT>::kBytes;
   int64_t t;
   int c;

@@ -97,12 +97,6 @@ __device__ __forceinline__ void block_range(const DispatchParams& p, int b, int 
   if (f1 > p.seg_entry[s + 1]) f1 = p.seg_entry[s + 1];
 }
 
-// Replica count of e clamped to the table width (keeps every table read in
-// bounds); a count outside [1, rmax] is reported by count_kernel's block 0.
-__device__ __forceinline__ int reps(const DispatchParams& p, int e) {
-  const int r = p.n_rep[e];
-  return r < 1 ? 1 : (r > p.rmax ? p.rmax : r);
-}
 
 // rr mod R with the sign of R (torch's % on int64 tensors, ep.py:94), in [0, R)
 __device__ __forceinline__ int floor_mod(int64_t rr, int R) {
@@ -332,7 +326,9 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(DispatchParams p) {
     for (int i = tid; i < E * p.rmax; i += kThreads) s_tab[i] = p.table[i];
   const int my_nrep = tid < E ? p.n_rep[tid] : 1;
   if (tid < E) {
-    s_R[tid] = my_nrep < 1 ? 1 : (my_nrep > p.rmax ? p.rmax : my_nrep);   // reps(): clamped to [1, rmax]
+    // replica count clamped to the table width (keeps every table read in
+    // bounds); a count outside [1, rmax] is reported by block 0
+    s_R[tid] = my_nrep < 1 ? 1 : (my_nrep > p.rmax ? p.rmax : my_nrep);
     s_g2l[tid] = p.g2l[tid];
   }
   // round-robin counters of (segment, expert) i = tid + u kThreads; one launch

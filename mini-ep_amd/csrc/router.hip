@@ -495,7 +495,7 @@ __global__ __launch_bounds__(kWaves * 64) void router_kernel(const typename Elem
 template <int NSEG>
 __device__ __forceinline__ void router32_logits(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
                                                 int64_t n_tokens, int64_t t0, unsigned char* ws, f32x4 (&acc)[2]) {
-  constexpr int E = 32, NF = 2, H = 1024 * NSEG;
+  constexpr int NF = 2, H = 1024 * NSEG;
   constexpr int kRowStride = 1024 * 2 + 16;        // bytes of one W_r row segment in LDS (16 B pad: conflict-free)
   const int tid = threadIdx.x, lane = lane_id();
   const int r = lane & 15, g = lane >> 4;
@@ -607,9 +607,6 @@ struct FusedDispatch {
   const uint8_t* valid;     // (N,) or NULL
 };
 
-__device__ __forceinline__ int load_dev(const int32_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 __device__ __forceinline__ uint32_t load_dev(const uint32_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
