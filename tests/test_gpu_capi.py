@@ -11,7 +11,7 @@ from miniep_amd import HipMoEBackend, _lib, route, workloads
 pytestmark = pytest.mark.gpu
 
 
-def _moe_layer_raw(L, x, w_r, w_in, w_out, k=8):
+def _moe_layer_raw(L, x, w_r, w_in, w_out, k=8, one_call=False):
     vp, i64 = ctypes.c_void_p, ctypes.c_int64
     N, H = x.shape
     E = w_r.shape[0]
@@ -43,30 +43,43 @@ def _moe_layer_raw(L, x, w_r, w_in, w_out, k=8):
     act = torch.empty(L.mep_experts_workspace_size(N * k, I, BF16), dtype=torch.uint8, device="cuda")
     y = torch.empty(N * k, H, dtype=x.dtype, device="cuda")
     queue = torch.zeros(L.mep_experts_queue_ints(N * k, E), dtype=torch.int32, device="cuda")
-    ok(L.mep_grouped_swiglu(x.data_ptr(), N, k, perm.data_ptr(), offsets.data_ptr(), E, N * k, w_in.data_ptr(),
-                            w_out.data_ptr(), H, I, BF16, y.data_ptr(), act.data_ptr(), act.numel(),
-                            queue.data_ptr(), queue.numel(), s))
+    out = torch.empty(N, H, dtype=x.dtype, device="cuda")
+    if one_call:
+        ok(L.mep_grouped_swiglu_combine(x.data_ptr(), N, k, perm.data_ptr(), offsets.data_ptr(), row.data_ptr(),
+                                        gate.data_ptr(), None, E, N * k, w_in.data_ptr(), w_out.data_ptr(), H, I,
+                                        BF16, y.data_ptr(), act.data_ptr(), act.numel(), queue.data_ptr(),
+                                        queue.numel(), out.data_ptr(), s))
+    else:
+        ok(L.mep_grouped_swiglu(x.data_ptr(), N, k, perm.data_ptr(), offsets.data_ptr(), E, N * k,
+                                w_in.data_ptr(), w_out.data_ptr(), H, I, BF16, y.data_ptr(), act.data_ptr(),
+                                act.numel(), queue.data_ptr(), queue.numel(), s))
     ok(L.mep_experts_check(queue.data_ptr(), s))
     assert int(queue.abs().sum()) == 0                   # every launch leaves the schedule words at zero
-    out = torch.empty(N, H, dtype=x.dtype, device="cuda")
-    ok(L.mep_combine(y.data_ptr(), gate.data_ptr(), row.data_ptr(), None, N, k, H, BF16, out.data_ptr(), s))
+    if not one_call:
+        ok(L.mep_combine(y.data_ptr(), gate.data_ptr(), row.data_ptr(), None, N, k, H, BF16, out.data_ptr(), s))
     return out, idx, gate
 
 
-def test_raw_ctypes_layer_matches_backend():
-    banner("raw C ABI layer")
+@pytest.mark.parametrize("n", [2048, 32])
+def test_raw_ctypes_layer_matches_backend(n):
+    """2048 tokens: the tiled experts launch; 32 tokens: the small-batch
+    launch, which mep_grouped_swiglu_combine ends with the combine.  The raw
+    calls (experts + combine as two calls, and as one) give the backend's
+    bits."""
+    banner(f"raw C ABI layer, {n} tokens")
     L = _lib.lib()          # signatures are registered by the loader
-    layer = workloads.make_layer(2048, seed=9, zipf_s=1.2)
+    layer = workloads.make_layer(n, seed=9, zipf_s=1.2 if n > 1000 else 0.0)
     bf = torch.bfloat16
     x = layer.x.to(bf).cuda()
     w_r = layer.w_router.to(bf).cuda()
     w_in = layer.w_in.to(bf).cuda()
     w_out = layer.w_out.to(bf).cuda()
     out, idx, gate = _moe_layer_raw(L, x, w_r, w_in, w_out)
+    out1, _, _ = _moe_layer_raw(L, x, w_r, w_in, w_out, one_call=True)
     idx2, gate2 = route(x, w_r, 8)
     ref = HipMoEBackend(w_in, w_out)(x, idx2, gate2)
     assert torch.equal(idx, idx2) and torch.equal(gate, gate2)
-    assert torch.equal(out, ref)
+    assert torch.equal(out, ref) and torch.equal(out1, ref)
 
 
 def test_error_codes_and_messages():

@@ -336,7 +336,7 @@ def test_other_shapes_vs_oracle(H, I, E, k, n, dtype):
     assert err <= (TOL_BF16 if bf else TOL_F32)
 
 
-@pytest.mark.parametrize("case", ["decode_t32", "masked_t100", "zipf_t128", "e64_t16", "h256_t32",
+@pytest.mark.parametrize("case", ["decode_t32", "masked_t100", "zipf_t128", "e64_t16", "h256_t32", "h2048_t40",
                                   "bf16_t3000", "f32_t32"])
 def test_grouped_swiglu_combine_equals_two_calls(case):
     """mep_grouped_swiglu_combine: for small bf16 top-8 batches the
@@ -344,14 +344,16 @@ def test_grouped_swiglu_combine_equals_two_calls(case):
     GEMM-2 workgroup's y stores, then sum in combine8's order); other sizes
     and fp32 make the two calls.  The layer output equals grouped_swiglu +
     combine bit for bit, masked tokens included, on two inputs in a row
-    through the same buffers, and the schedule words return to zero."""
+    through the same buffers, and the schedule words return to zero.
+    h2048: 2048-wide rows and K = 1024 in GEMM-2 (weight steps past those in
+    LDS)."""
     banner(f"experts + combine in one call vs two: {case}")
     dt = torch.float32 if case.startswith("f32") else torch.bfloat16
     g = torch.Generator().manual_seed(33)
     E = 64 if case.startswith("e64") else 32
     n = int(case.split("_t")[1])
-    H = 256 if case.startswith("h256") else 1024
-    I = 256 if case.startswith("h256") else 512
+    H = 256 if case.startswith("h256") else (2048 if case.startswith("h2048") else 1024)
+    I = 256 if case.startswith("h256") else (1024 if case.startswith("h2048") else 512)
     valid = (torch.rand(n, generator=g) < 0.7) if case.startswith("masked") else None
     if case.startswith("zipf"):
         L = workloads.make_layer(n, seed=33, zipf_s=1.2)
