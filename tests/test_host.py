@@ -51,6 +51,27 @@ def test_dispatch_rejects_missing_outputs_before_launch():
     assert call(64, 4, fake, fake, None) == _lib.ERR_INVALID_ARG
 
 
+def test_experts_combine_rejects_bad_arguments_before_launch():
+    """mep_grouped_swiglu_combine checks on the host that y_entries covers
+    every (token, slot) cell (max_rows = n_tokens * top_k) and that the
+    combine's inputs and output are given, before anything is enqueued.
+    (Placeholder pointers, never dereferenced.)"""
+    L = _lib.lib()
+    fake = 4096
+    BF16 = 1
+
+    def call(n, max_rows, row, gate, out):
+        return L.mep_grouped_swiglu_combine(fake, n, 8, fake, fake, row, gate, None, 32, max_rows, fake, fake,
+                                            1024, 512, BF16, fake, fake, 1 << 30, fake, 1 << 20, out, None)
+
+    assert call(32, 255, fake, fake, fake) == _lib.ERR_INVALID_ARG
+    assert b"max_rows" in L.mep_last_error()
+    for row, gate, out in ((None, fake, fake), (fake, None, fake), (fake, fake, None)):
+        assert call(32, 256, row, gate, out) == _lib.ERR_INVALID_ARG
+        assert b"null" in L.mep_last_error()
+    assert call(0, 0, None, None, None) == 0          # nothing to do: no pointer is needed
+
+
 def test_workspace_size_queries():
     L = _lib.lib()
     seg = (ctypes.c_int64 * 2)(0, 16384)
