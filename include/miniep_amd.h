@@ -351,6 +351,36 @@ int mep_combine_rows(const void* y_rows, const void* topk_gate, const int32_t* r
                      const uint8_t* valid_mask, int64_t n_tokens, int32_t top_k,
                      int32_t hidden, int32_t dtype, void* out, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Test hook, no counterpart in the reference: makes one of the bounded waits
+ * of the one-launch kernels give up, so that tests can drive the give-up
+ * path from the host (every wait still ends, every kernel exits).  While a
+ * site is set, launches of that kind use `polls` as their poll limit and:
+ *   MEP_GIVEUP_DISPATCH  the last workgroup of a one-launch dispatch
+ *                        (mep_dispatch, mep_route_dispatch) withholds its
+ *                        per-expert counts, so every workgroup gives up;
+ *   MEP_GIVEUP_ROWS      GEMM-2 tiles of row tile 0 of the tiled one-launch
+ *                        experts wait for one GEMM-1 count more than exists;
+ *   MEP_GIVEUP_CHUNK     GEMM-2 workgroups of chunk 0 of the small-batch one
+ *                        launch wait for one GEMM-1 count more than exists;
+ *   MEP_GIVEUP_COMBINE   combine workgroup 0 of the small-batch launch that
+ *                        ends with the combine waits for one GEMM-2
+ *                        workgroup more than exists.
+ * A give-up is reported as in normal operation (mep_dispatch_check,
+ * mep_experts_check) and poisons what the caller consumes: a dispatch sets
+ * offsets[n_local] = -1 and every row_of_entry to -2 (the experts kernels then
+ * run no tile, the combine writes NaN for such tokens); a GEMM-2 tile or
+ * workgroup writes NaN rows; a combine workgroup writes NaN outputs.
+ * MEP_GIVEUP_NONE (0) restores normal operation.  Process-wide setting, read
+ * when a launch is enqueued; not for concurrent use.
+ * ---------------------------------------------------------------------- */
+#define MEP_GIVEUP_NONE 0
+#define MEP_GIVEUP_DISPATCH 1
+#define MEP_GIVEUP_ROWS 2
+#define MEP_GIVEUP_CHUNK 3
+#define MEP_GIVEUP_COMBINE 4
+int mep_test_force_giveup(int32_t site, int32_t polls);
+
 #ifdef __cplusplus
 }
 #endif

@@ -69,6 +69,7 @@ __global__ __launch_bounds__(kThreads) void combine_kernel(const typename Elem<D
   int c;
   if (!chunk_of_thread(n_tokens, hidden / EPC, t, c)) return;
   const bool tok_ok = valid == nullptr || valid[t] != 0;
+  bool poison = false;                                  // an entry of a dispatch that gave up: NaN
   float acc[EPC];
 #pragma unroll
   for (int q = 0; q < EPC; ++q) acc[q] = 0.0f;
@@ -76,6 +77,7 @@ __global__ __launch_bounds__(kThreads) void combine_kernel(const typename Elem<D
 #pragma unroll 8
     for (int s = 0; s < k; ++s) {
       const int32_t row = row_of_entry[t * k + s];
+      poison |= row == kPoisonRow;
       if (row < 0) continue;                            // cell computed elsewhere
       const float g = Elem<DT>::to_f32(gate[t * k + s]);
       const int64_t cell = INDEXED ? static_cast<int64_t>(row) : t * k + s;
@@ -84,6 +86,8 @@ __global__ __launch_bounds__(kThreads) void combine_kernel(const typename Elem<D
       accumulate_cell<DT>(acc, g, v);
     }
   }
+#pragma unroll
+  for (int q = 0; q < EPC; ++q) acc[q] = poison ? __builtin_nanf("") : acc[q];
   *reinterpret_cast<u32x4*>(out + t * hidden + c * EPC) = pack_row_chunk<DT>(acc);
 }
 

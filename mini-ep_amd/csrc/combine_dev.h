@@ -9,7 +9,8 @@
 // caller picks the cache policy); the 8 cells, their row_of_entry entries,
 // the gates and the valid flag are independent loads issued together, and an
 // absent cell is skipped with a select, so whatever it holds never reaches
-// the sum.
+// the sum.  A token with a poisoned entry (kPoisonRow: its dispatch gave up)
+// gets NaN.
 #pragma once
 
 #include "common.h"
@@ -54,12 +55,14 @@ __device__ __forceinline__ void combine8_chunk(const typename Elem<DT>::T* __res
     g[s] = Elem<DT>::to_f32(gate[t * K + s]);
   }
   const bool tok_ok = valid == nullptr || valid[t] != 0;
+  bool poison = false;
   float acc[EPC];
 #pragma unroll
   for (int q = 0; q < EPC; ++q) acc[q] = 0.0f;
 #pragma unroll
   for (int s = 0; s < K; ++s) {
     const bool here = tok_ok && row[s] >= 0;
+    poison |= row[s] == kPoisonRow;
     float yv[EPC];
     if constexpr (DT == MEP_DTYPE_BF16) {
       const uint32_t w[4] = {v[s].x, v[s].y, v[s].z, v[s].w};
@@ -80,6 +83,8 @@ __device__ __forceinline__ void combine8_chunk(const typename Elem<DT>::T* __res
       acc[q] = here ? sum : acc[q];
     }
   }
+#pragma unroll
+  for (int q = 0; q < EPC; ++q) acc[q] = poison ? __builtin_nanf("") : acc[q];
   *reinterpret_cast<u32x4*>(out + t * hidden + c * EPC) = pack_row_chunk<DT>(acc);
 }
 

@@ -85,6 +85,65 @@ hipError_t launch_route_dispatch_fused(const void* x, const void* w, int64_t n, 
 // waiting for another's histogram row
 constexpr uint32_t kFlagBarrier = 8u;
 
+// Header of a dispatch workspace: four 128-byte lines, then the status flags.
+// Word 0: the number of launched blocks; kEpochWord: the epoch of the
+// one-launch exchange (its tags); kDoneWord: workgroups of the current
+// one-launch call that have finished; kGiveupWord: nonzero once one of them
+// gave up waiting.  The last two are zero between calls.
+constexpr int kWsHeaderBytes = 512;
+constexpr int kEpochWord = 32, kDoneWord = 64, kGiveupWord = 96;
+
+// row_of_entry value of an entry of a one-launch dispatch that gave up (a
+// workgroup waited too long for another's counts): the call's placement is
+// invalid, offsets[n_local] is -1 (the experts kernels then run no tile) and
+// the combine writes NaN for the token.
+constexpr int32_t kPoisonRow = -2;
+
+// Test hook (mep_test_force_giveup): the bounded wait that launches force to
+// give up, and its poll limit; site 0 is normal operation.
+struct GiveupTest {
+  int site;
+  int polls;
+};
+GiveupTest giveup_test();
+
+// End of a workgroup of a one-launch dispatch exchange, called by every lane
+// of wave 0 after a barrier that follows all of the workgroup's stores.  Lane
+// 0 records a give-up in the header, then counts the workgroup finished.  The
+// last workgroup of the call to finish (by then every other one has read the
+// epoch and completed its stores) returns both words to zero and gets
+// kExchangeLast, plus kExchangeGaveUp if any workgroup gave up; the others
+// get 0.  Only the last workgroup may advance the epoch: a workgroup that was
+// not resident with the others can start after the early ones have exited,
+// and must still read this call's epoch.
+constexpr int kExchangeLast = 1, kExchangeGaveUp = 2;
+__device__ __forceinline__ int finish_exchange(uint32_t* header, bool gave_up, int n_blocks) {
+  int r = 0;
+  if ((threadIdx.x & 63) == 0) {
+    if (gave_up) __hip_atomic_fetch_or(header + kGiveupWord, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): the give-up is recorded before the count
+    const uint32_t done =
+        __hip_atomic_fetch_add(header + kDoneWord, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (done == static_cast<uint32_t>(n_blocks - 1)) {
+      const uint32_t g = __hip_atomic_exchange(header + kGiveupWord, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(header + kDoneWord, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      r = kExchangeLast | (g != 0u ? kExchangeGaveUp : 0);
+    }
+  }
+  return __shfl(r, 0, 64);
+}
+
+// The poison of a one-launch dispatch that gave up (the last workgroup's
+// wave 0): every row_of_entry entry kPoisonRow, offsets[n_local] = -1, with
+// device-scope stores (the values they replace were stored that way too).
+__device__ __forceinline__ void poison_dispatch(int32_t* row_of_entry, int64_t n_entries, int32_t* offsets,
+                                                int n_local) {
+  const int lane = threadIdx.x & 63;
+  for (int64_t f = lane; f < n_entries; f += 64)
+    __hip_atomic_store(row_of_entry + f, kPoisonRow, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (lane == 0) __hip_atomic_store(offsets + n_local, -1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 inline int dtype_bytes(int dtype) {
   return dtype == MEP_DTYPE_F32 ? 4 : (dtype == MEP_DTYPE_BF16 ? 2 : 0);
 }

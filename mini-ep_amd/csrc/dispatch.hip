@@ -76,6 +76,9 @@ struct DispatchParams {
   uint64_t* rows;       // [nbl * E] tagged per-block counts (one-launch dispatch)
   int scanned;          // 1: prefix_kernel turned bc into per-segment exclusive prefixes
   int nb, nbl, n_seg;
+  // one launch: polls of a tagged word before a workgroup gives up, and the
+  // block that withholds its counts (test hook; -1: none)
+  int tag_polls, dbg_withhold;
   int64_t seg_entry[kMaxSeg + 1];
   int seg_block[kMaxSeg + 1];
 };
@@ -224,8 +227,9 @@ constexpr int kTabLds = 2048;
 // round-robin counters below 2^32) has a clear top bit in its high word, so a
 // workspace zero-filled once serves calls of any size.  All blocks must be
 // resident at once: the host launches it only when they fit.  A wait longer
-// than kTagPolls polls sets kFlagBarrier in the block's status word.
-constexpr int kEpochWord = 32;                   // header word of the epoch (its own 128-byte line)
+// than kTagPolls polls sets kFlagBarrier in the block's status word; the
+// block then places nothing (its entries get kPoisonRow) and, as the last
+// block to finish sees, the whole call is poisoned (see finish_exchange).
 constexpr int kTagPolls = 1 << 20;
 
 __device__ __forceinline__ uint32_t load_dev(const uint32_t* q) {
@@ -243,10 +247,10 @@ __device__ __forceinline__ void store_dev(uint32_t* q, uint32_t v) {
 
 // Reads the tagged words w[i * stride] for i in [0, n) (this thread's share:
 // i = first, first + step, ...), each re-read until it carries `tag`, and
-// calls use(i, count) for each.  Sets *bad after kTagPolls polls of a batch.
+// calls use(i, count) for each.  Sets *bad after `polls` polls of a batch.
 template <typename Use>
 __device__ __forceinline__ void read_tagged(const uint64_t* w, int64_t stride, int first, int n, int step,
-                                            uint64_t tag, uint32_t* bad, Use use) {
+                                            uint64_t tag, int polls, uint32_t* bad, Use use) {
   constexpr int kBatch = 8;
   for (int i0 = first; i0 < n; i0 += step * kBatch) {
     uint64_t v[kBatch];
@@ -260,7 +264,7 @@ __device__ __forceinline__ void read_tagged(const uint64_t* w, int64_t stride, i
 #pragma unroll
       for (int u = 0; u < kBatch; ++u) stale |= (v[u] & ~0xffffffffull) != tag;
       if (!stale) break;
-      if (it >= kTagPolls) { *bad = kFlagBarrier; break; }
+      if (it >= polls) { *bad = kFlagBarrier; break; }
       __builtin_amdgcn_s_sleep(1);
 #pragma unroll
       for (int u = 0; u < kBatch; ++u)
@@ -291,6 +295,7 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(DispatchParams p) {
   __shared__ uint32_t flag;
   __shared__ int s_cnt[FUSED ? kMaxExperts : 1];  // one launch: this block's entries per expert
   __shared__ uint32_t cflag;                      // one launch: this block's count-pass flags
+  __shared__ uint32_t s_bad;                      // one launch: a wait of this block gave up
 
   const int b = blockIdx.x, tid = threadIdx.x;
   const int E = p.E;
@@ -349,7 +354,7 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(DispatchParams p) {
   if (tid == 0) flag = 0;
   if constexpr (FUSED) {
     for (int e = tid; e < E; e += kThreads) s_cnt[e] = 0;
-    if (tid == 0) cflag = 0;
+    if (tid == 0) { cflag = 0; s_bad = 0; }
   }
   __syncthreads();
   if (tid < E) {
@@ -385,8 +390,9 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(DispatchParams p) {
     if (key < E) atomicAdd(&s_cnt[key], 1);
     if (bad_id) atomicOr(&cflag, kFlagRange);
     __syncthreads();
-    for (int e = tid; e < E; e += kThreads)
-      store_dev(p.rows + static_cast<int64_t>(b) * E + e, tag | static_cast<uint32_t>(s_cnt[e]));
+    if (b != p.dbg_withhold)
+      for (int e = tid; e < E; e += kThreads)
+        store_dev(p.rows + static_cast<int64_t>(b) * E + e, tag | static_cast<uint32_t>(s_cnt[e]));
     // every block's counts: the segment totals, and my prefix (the earlier
     // blocks of my segment)
     const int parts = kThreads / E > 0 ? kThreads / E : 1;
@@ -394,7 +400,7 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(DispatchParams p) {
     if (part < parts && tid < parts * E) {
       int my_pre = 0;
       int sg = 0, sg_end = p.seg_block[1], run = 0;   // this thread's rows come in increasing order
-      read_tagged(p.rows + e, E, part, p.nb, parts, tag, &tag_bad, [&](int bb, int c) {
+      read_tagged(p.rows + e, E, part, p.nb, parts, tag, p.tag_polls, &tag_bad, [&](int bb, int c) {
         while (bb >= sg_end) {
           if (run) atomicAdd(&segtot[sg][e], run);
           run = 0;
@@ -407,8 +413,12 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(DispatchParams p) {
       if (run) atomicAdd(&segtot[sg][e], run);
       atomicAdd(&pre[e], my_pre);
     }
+    if (tag_bad) s_bad = tag_bad;
   }
   __syncthreads();
+  // a block whose wait gave up has counts from earlier calls: it places
+  // nothing and leaves rr and route_counts alone
+  const bool gave_up = FUSED && s_bad != 0u;
 
   // 1. segment totals and my prefix: from the tagged counts above (one
   // launch), read from prefix_kernel's results, or
@@ -496,10 +506,12 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(DispatchParams p) {
   }
   if (b == 0) {
     for (int j = tid; j <= p.n_local; j += kThreads) {
-      p.offsets[j] = lpre[j];
+      // one launch: device scope, as is the poison that may replace offsets[n_local]
+      if (FUSED) store_dev(reinterpret_cast<uint32_t*>(p.offsets + j), static_cast<uint32_t>(lpre[j]));
+      else p.offsets[j] = lpre[j];
       if (j < p.n_local) p.counts[j] = lcount[j];
     }
-    for (int e = tid; e < E; e += kThreads) {
+    for (int e = gave_up ? E : tid; e < E; e += kThreads) {
       int64_t tot = 0;
       for (int sg = 0; sg < p.n_seg; ++sg) {
         tot += segtot[sg][e];
@@ -510,12 +522,23 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(DispatchParams p) {
   }
   __syncthreads();
 
-  // 3. rank this block's entries in flat order and scatter
+  // 3. rank this block's entries in flat order and scatter.  One launch:
+  // row_of_entry with device-scope stores, as is the poison that may replace it.
+  auto put_row = [&](int64_t ff, int32_t v) {
+    if (FUSED) store_dev(reinterpret_cast<uint32_t*>(p.row_of_entry + ff), static_cast<uint32_t>(v));
+    else p.row_of_entry[ff] = v;
+  };
   const int lane = tid & 63, wave = tid >> 6;
   const int nbits = 32 - __clz(E);
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  if (gave_up) {
+    if (f < f1) {
+      put_row(f, kPoisonRow);
+      if (p.dest != nullptr) p.dest[f] = -1;
+    }
+  } else {
   if (dropped) {
-    p.row_of_entry[f] = -1;
+    put_row(f, -1);
     if (p.dest != nullptr) p.dest[f] = -1;
   }
   uint64_t peers = ~0ull;
@@ -549,7 +572,8 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(DispatchParams p) {
         atomicOr(&flag, kFlagResident);
       }
     }
-    p.row_of_entry[f] = row;
+    put_row(f, row);
+  }
   }
   if (FUSED && tag_bad) atomicOr(&flag, tag_bad);
   __syncthreads();
@@ -560,8 +584,15 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(DispatchParams p) {
       const uint32_t f = flag | (FUSED ? cflag : p.flags[b]);   // this block's count and scatter flags
       if (f != 0u) atomicOr(p.status, f);
     }
-    // every block's counts have been read, so every block has read the epoch
-    if (FUSED && b == 0) store_dev(p.header + kEpochWord, static_cast<uint32_t>(tag >> 32) & 0x7fffffffu);
+  }
+  if constexpr (FUSED) {
+    // the last block to finish poisons a call in which a block gave up, and
+    // advances the epoch (every block has read it)
+    if (tid < 64) {
+      const int r = finish_exchange(p.header, gave_up, static_cast<int>(gridDim.x));
+      if (r & kExchangeGaveUp) poison_dispatch(p.row_of_entry, p.seg_entry[p.n_seg], p.offsets, p.n_local);
+      if ((r & kExchangeLast) && tid == 0) store_dev(p.header + kEpochWord, static_cast<uint32_t>(tag >> 32) & 0x7fffffffu);
+    }
   }
 }
 
@@ -574,7 +605,7 @@ struct WsLayout {
 WsLayout ws_layout(int nbl, int n_seg, int E) {
   WsLayout l;
   l.header = 0;
-  l.flags = 256;
+  l.flags = kWsHeaderBytes;
   l.rr_snap = align_up(l.flags + sizeof(uint32_t) * 2 * nbl, 256);
   l.bc = align_up(l.rr_snap + sizeof(int64_t) * n_seg * E, 256);
   l.segtot = align_up(l.bc + sizeof(int32_t) * static_cast<size_t>(nbl) * E, 256);
@@ -739,6 +770,9 @@ int dispatch_impl(const char* fn, const int64_t* topk_idx, const uint8_t* valid_
   for (int s = n_segments + 1; s <= kMaxSeg; ++s) { p.seg_entry[s] = p.seg_entry[n_segments]; p.seg_block[s] = p.nb; }
 
   p.rows = reinterpret_cast<uint64_t*>(ws + l.rows);
+  const GiveupTest gt = giveup_test();
+  p.tag_polls = gt.site == MEP_GIVEUP_DISPATCH ? gt.polls : kTagPolls;
+  p.dbg_withhold = gt.site == MEP_GIVEUP_DISPATCH ? p.nbl - 1 : -1;
 
   hipStream_t st = static_cast<hipStream_t>(stream);
   // one launch when every block fits on the device at once
@@ -894,6 +928,8 @@ extern "C" int mep_route_dispatch(const void* x, const void* w_router, const uin
   p.bc = reinterpret_cast<int32_t*>(ws + l.bc);
   p.segtot = reinterpret_cast<int32_t*>(ws + l.segtot);
   p.scanned = p.nb > kScanBlocks ? 1 : 0;
+  p.tag_polls = kTagPolls;
+  p.dbg_withhold = -1;
   p.n_seg = 1;
   p.seg_entry[0] = 0;
   for (int s = 1; s <= kMaxSeg; ++s) p.seg_entry[s] = n_tokens * top_k;
@@ -919,7 +955,7 @@ extern "C" int mep_dispatch_check(const void* workspace, void* stream) {
               "mep_dispatch_check: workspace holds no dispatch result");
   uint32_t acc = 0;
   uint32_t buf[1024];
-  const char* flags = static_cast<const char*>(workspace) + 256;
+  const char* flags = static_cast<const char*>(workspace) + kWsHeaderBytes;
   for (uint32_t i = 0; i < 2 * nbl; i += 1024) {
     const uint32_t n = (2 * nbl - i) < 1024 ? (2 * nbl - i) : 1024;
     e = hipMemcpy(buf, flags + sizeof(uint32_t) * i, sizeof(uint32_t) * n, hipMemcpyDeviceToHost);

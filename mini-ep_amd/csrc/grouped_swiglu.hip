@@ -85,6 +85,9 @@ struct GemmParams {
   uint32_t a_bytes;          // size of A in bytes (< 4 GiB)
   uint32_t k_magic;          // entry / top_k == umulhi(entry, k_magic) >> k_shift for entry < 2^31
   int k_shift;
+  int* flags;                // error flags word of the schedule buffer (sched::kFlags), or NULL
+  int wait_limit;            // small-batch one launch: polls before a wait gives up
+  int dbg_chunk;             // ... whose GEMM-2 waits for one count more (test hook; -1: none)
 };
 
 // Round-up reciprocal for exact division by d of every n < 2^31: with
@@ -126,6 +129,10 @@ __device__ void scan_units(const int* off, int* pre, int nl, int mult) {
   }
   if (lane == 0) pre[0] = 0;
 }
+
+// error flag of the schedule buffer: the offsets came from a dispatch that
+// gave up (sched::kFlagInput)
+constexpr int kFlagInputBit = 4;
 
 constexpr int pow2_floor(int v) { int r = 1; while (r * 2 <= v) r *= 2; return r; }
 
@@ -177,7 +184,12 @@ __global__ __launch_bounds__(Cfg::NT) void grouped_gemm_kernel(GemmParams p) {
   const int nl = p.n_local;
 
   // ---- tile table: tiles per expert, prefix over experts ---------------------
-  for (int j = tid; j <= nl; j += NT) s_off[j] = p.offsets[j];
+  // (offsets[nl] < 0: the dispatch gave up; no expert has rows, the call is flagged)
+  {
+    const int last = p.offsets[nl];
+    for (int j = tid; j <= nl; j += NT) s_off[j] = last < 0 ? 0 : p.offsets[j];
+    if (last < 0 && blockIdx.x == 0 && tid == 0 && p.flags != nullptr) atomicOr(p.flags, kFlagInputBit);
+  }
   __syncthreads();
   if (tid < 64) scan_units<BM>(s_off, s_prefix, nl, p.n_tiles_n);
   __syncthreads();
@@ -482,7 +494,7 @@ constexpr int TABLES = STG + NW * STG_WAVE;
 // row tile -> expert, one byte each, for launches of at most RT_TAB row
 // tiles (T <= 256k tokens at top-8); larger ones search the prefix table
 constexpr int RT_TAB = 8192;
-constexpr int LDS_BYTES = TABLES + (2 * (NLMAX + 1) + 2 * BM + 4 + NLMAX) * 4 + RT_TAB;
+constexpr int LDS_BYTES = TABLES + (2 * (NLMAX + 1) + 2 * BM + 8 + NLMAX) * 4 + RT_TAB;
 static_assert(LDS_BYTES <= 160 * 1024, "LDS budget of one workgroup");
 // buffer resource word 3 for raw 32-bit buffer access on gfx9-family parts
 constexpr int kBufWord3 = 0x00020000;
@@ -496,10 +508,14 @@ static_assert(BPW == NF, "one DMA block per MFMA group of an odd step");
 //   [0, 8)           items taken from each XCD's queue
 //   8                workgroups finished
 //   9                items computed
-//   10               error flags, sticky (never cleared by a launch):
+//   10               error flags, sticky (never cleared by a launch;
+//                    mep_experts_check reads and clears them):
 //                    kFlagWait  a GEMM-2 tile gave up waiting for its rows
-//                               (or the combine for GEMM-2's)
+//                               (or the combine for GEMM-2's); its
+//                               outputs are NaN
 //                    kFlagDrain items computed != items listed (never expected)
+//                    kFlagInput offsets[n_local] < 0: the dispatch gave up,
+//                               no tile ran
 //   11               bit per drained queue
 //   12, 13           small-batch launch ending with the combine: GEMM-2
 //                    workgroups done, combine workgroups past their wait
@@ -508,7 +524,7 @@ static_assert(BPW == NF, "one DMA block per MFMA group of an odd step");
 namespace sched {
 constexpr int kQueue = 0, kDone = 8, kItems = 9, kFlags = 10, kDrained = 11, kG2Done = 12, kCombDone = 13,
               kRowDone = 16;
-constexpr int kFlagWait = 1, kFlagDrain = 2;
+constexpr int kFlagWait = 1, kFlagDrain = 2, kFlagInput = kFlagInputBit;
 constexpr int kWaitLimit = 1 << 20;            // polls of one row counter (about a second)
 // the small-batch launch of both GEMMs runs up to this many rows
 constexpr int64_t kSmallRows = 1024;
@@ -538,6 +554,8 @@ struct MoeParams {
   int k_shift;
   int n_queues;              // queues (XCDs), a power of two <= 8
   int* sched;
+  int wait_limit;            // polls of a row counter before a GEMM-2 tile gives up
+  int dbg_row;               // row tile whose GEMM-2 tiles wait for one count more (test hook; -1: none)
 };
 
 // 16x16x32 bf16 MFMA with the accumulator in VGPRs; src0 = weight
@@ -607,7 +625,8 @@ __device__ __forceinline__ void buffer_lds_16(const unsigned char* base, int byt
 // holds no unfinished tile, and the tiles it waits for come earlier in the
 // queue than the one it waits with (fixed slots come before claimed ones),
 // so every wait ends.  A wait that still
-// exceeds sched::kWaitLimit polls sets sched flag kFlagWait and goes on.
+// exceeds p.wait_limit polls (sched::kWaitLimit) sets sched flag kFlagWait,
+// and the tile then stores NaN.
 // Which workgroup computes a tile never changes its result, so the bits are
 // those of two separate launches.
 // Device-scope atomics of a single lane (thread 0 of a workgroup).  The
@@ -665,8 +684,8 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(MoeParams p) {
   int* const s_prefix = reinterpret_cast<int*>(smem + TABLES);         // [NLMAX + 1] row tiles before expert j
   int* const s_off = s_prefix + NLMAX + 1;                             // [NLMAX + 1] row offsets
   int* const s_rows = s_off + NLMAX + 1;                               // [2][BM] row maps
-  int* const s_msg = s_rows + 2 * BM;                                  // [4] answers of thread 0's atomics
-  int* const s_slot = s_msg + 4;                                       // [NLMAX] weight slot of expert j
+  int* const s_msg = s_rows + 2 * BM;                                  // [8] answers of thread 0's atomics
+  int* const s_slot = s_msg + 8;                                       // [NLMAX] weight slot of expert j
   unsigned char* const s_rt_e = reinterpret_cast<unsigned char*>(s_slot + NLMAX);   // [RT_TAB] expert of row tile R
 
   const int tid = threadIdx.x;
@@ -689,7 +708,13 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(MoeParams p) {
   auto claim = [&](int qq) { return n_static + atomic_add_1(sched + sched::kQueue + qq, 1); };
 
   // ---- row tiles ------------------------------------------------------------------
-  for (int j = tid; j <= nl; j += NT) s_off[j] = p.offsets[j];
+  // offsets[nl] < 0: the dispatch gave up (its outputs are poisoned); then no
+  // expert has rows, no tile runs and the call is flagged
+  {
+    const int last = p.offsets[nl];
+    for (int j = tid; j <= nl; j += NT) s_off[j] = last < 0 ? 0 : p.offsets[j];
+    if (last < 0 && blockIdx.x == 0 && tid == 0) atomic_or_1(sched + sched::kFlags, sched::kFlagInput);
+  }
   for (int j = tid; j < nl; j += NT) s_slot[j] = p.w_slot != nullptr ? p.w_slot[j] : j;
   __syncthreads();
   if (tid < 64) scan_units<BM>(s_off, s_prefix, nl, 1);
@@ -750,16 +775,21 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(MoeParams p) {
     t.act_wm = (t.row_end - t.row0 <= BM / 2) ? 2 : 4;
     return t;
   };
-  // thread 0: until row tile R's GEMM-1 tiles are all counted (bounded)
+  // GEMM-1 counts a GEMM-2 tile of row tile R waits for: n1 (one more for
+  // the test hook's row tile, which therefore gives up)
+  auto need = [&](int R) { return n1 + (R == p.dbg_row ? 1 : 0); };
+  // thread 0: until row tile R's GEMM-1 tiles are all counted (bounded);
+  // returns 1 if the wait gave up (the tile then stores NaN)
   auto wait_rows = [&](int R) {
     int polls = 0;
-    while (atomic_read(sched + sched::kRowDone + R) < n1) {
-      if (++polls == sched::kWaitLimit) {
+    while (atomic_read(sched + sched::kRowDone + R) < need(R)) {
+      if (++polls == p.wait_limit) {
         atomic_or_1(sched + sched::kFlags, sched::kFlagWait);
-        break;
+        return 1;
       }
       __builtin_amdgcn_s_sleep(4);
     }
+    return 0;
   };
   // row map: perm[row0 .. row0 + BM) of a tile DMA'd into LDS (clamped to the
   // tile's last row, so every lane reads inside perm).  GEMM-1 gathers its A
@@ -948,7 +978,7 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(MoeParams p) {
   // lines through a per-wave LDS slice.  No workgroup barrier: the stores
   // drain while the next tile's MFMAs run.
   typedef uint16_t T;
-  auto epilogue = [&](const Tile& t, int parity) {
+  auto epilogue = [&](const Tile& t, int parity, int poison) {
     if (wm >= t.act_wm) return;
     // the last MFMAs' results must be written before they are read (the
     // asm hides the MFMAs from the hazard recognizer): pad, then tie every
@@ -958,6 +988,14 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(MoeParams p) {
     for (int i = 0; i < MF; ++i)
 #pragma unroll
       for (int j = 0; j < NF; ++j) pin_acc(acc[i][j]);
+    // a GEMM-2 tile whose wait for its rows gave up stores NaN
+    if (poison) {
+      const float nan = __builtin_nanf("");
+#pragma unroll
+      for (int i = 0; i < MF; ++i)
+#pragma unroll
+        for (int j = 0; j < NF; ++j) acc[i][j] = f32x4{nan, nan, nan, nan};
+    }
     // per-lane terms from an opaque copy of the thread index, so the compiler
     // cannot hoist them out of the tile loop (they would be spilled there)
     int et = tid;
@@ -1150,11 +1188,12 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(MoeParams p) {
 #pragma unroll
       for (int i = 0; i < BPW; ++i) dma_blk(sc, 1, 1, i);
     }
-    if (BOTH && !cur.g1 && tid == 0) wait_rows(cur.R);
+    if (tid == 0) s_msg[4] = (BOTH && !cur.g1) ? wait_rows(cur.R) : 0;
     rowmap_dma(cur, 0);
     if (has_next) rowmap_dma(nxt, 1);
     __builtin_amdgcn_s_waitcnt(kVmcnt0);
     __syncthreads();
+    int poison = __builtin_amdgcn_readfirstlane(s_msg[4]);   // cur's wait gave up
     if (wave_a) {
       sc = setup(cur, 0);
 #pragma unroll
@@ -1242,20 +1281,20 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(MoeParams p) {
         if (g < n_items) {
           nxt = decode(g, cq);
           has_next = true;
-          ready = !nxt.g1 && (!BOTH || (!early && __builtin_amdgcn_readfirstlane(s_msg[2]) >= n1));
+          ready = !nxt.g1 && (!BOTH || (!early && __builtin_amdgcn_readfirstlane(s_msg[2]) >= need(nxt.R)));
           if (ready) rowmap_dma(nxt, (it + 1) & 1);     // read by its epilogue, many barriers on
         } else {
           open = false;
           if (tid == 0) atomic_or_1(sched + sched::kDrained, 1 << cq);
         }
       } else {
-        ready = has_next && (!poll || __builtin_amdgcn_readfirstlane(s_msg[2]) >= n1);
+        ready = has_next && (!poll || __builtin_amdgcn_readfirstlane(s_msg[2]) >= need(nxt.R));
       }
       sc = ready ? setup(nxt, (it + 1) & 1) : setup(cur, it & 1);
       step(S1, NO, YES, YES, sc, 0, 0, 1, act);          // step KT-3: next stage 0 -> buffer 0
       step(S0, NO, NO, YES, sc, 0, 0, 1, act);           // step KT-2
       step(S1, NO, YES, NO, sc, 1, 1, 0, act);           // step KT-1: next stage 1 -> buffer 1
-      epilogue(cur, it & 1);
+      epilogue(cur, it & 1, poison);
       ++n_done;
       if (BOTH && cur.g1) sig_r = cur.R;
       if (!has_next) {
@@ -1264,6 +1303,7 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(MoeParams p) {
         break;
       }
       cur = nxt;
+      poison = 0;
       has_next = false;
       if (ahead2) {
         const int g = __builtin_amdgcn_readfirstlane(s_msg[0]);
@@ -1283,12 +1323,13 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(MoeParams p) {
         __syncthreads();
         if (tid == 0) {
           if (BOTH && sig_r >= 0) atomic_add_1(sched + sched::kRowDone + sig_r, 1);
-          if (BOTH && !cur.g1) wait_rows(cur.R);
+          s_msg[4] = (BOTH && !cur.g1) ? wait_rows(cur.R) : 0;
         }
         sig_r = -1;
         rowmap_dma(cur, (it + 1) & 1);
         __builtin_amdgcn_s_waitcnt(kVmcnt0);
         __syncthreads();
+        poison = __builtin_amdgcn_readfirstlane(s_msg[4]);
         sc = setup(cur, (it + 1) & 1);
 #pragma unroll
         for (int i = 0; i < BPW; ++i) dma_blk(sc, 0, 0, i);
@@ -1365,6 +1406,8 @@ struct CombineParams {
   int hidden;
   int n_g2, n_comb;                // GEMM-2 and combine workgroups of the launch
   uint32_t y_bytes;                // bytes of y_entries (< 4 GiB)
+  int wait_limit;                  // polls before a combine workgroup's wait gives up
+  int dbg_comb;                    // combine workgroup that waits for one more (test hook; -1: none)
 };
 
 // One workgroup's share of a small-batch GEMM: a (chunk, column block) pair
@@ -1389,19 +1432,29 @@ struct CombineParams {
 // workgroups are dispatched in grid order, so every GEMM-1 workgroup is
 // resident before any GEMM-2 workgroup can wait, GEMM-1 never waits, and
 // every wait ends.  The last GEMM-2 workgroup of a chunk to pass the second
-// wait returns the chunk's two counters to zero.
+// wait takes the chunk's counts back out (the amounts every workgroup adds),
+// so they return to zero once every workgroup has finished, in any order.
+// A wait gives up after p.wait_limit polls: the wait flag is set and the
+// workgroup stores NaN.
 // COMB (GEMM-2 of a launch that ends with the combine): y is stored with
 // device scope, and every GEMM-2 workgroup, with rows or without, counts
 // itself done in `sched` once its stores are complete.
 template <bool GEMM1, bool FUSED, bool COMB = false>
 __device__ __forceinline__ void skinny_body(const GemmParams& p, int block, int n_cb_other, int* sched,
-                                            int* s_pre, int* s_off, unsigned char* s_w) {
+                                            int* s_pre, int* s_off, unsigned char* s_w, int* s_gave) {
   static_assert(!COMB || (FUSED && !GEMM1), "the combine follows the fused launch's GEMM-2");
   using namespace skinny;
   typedef uint16_t T;
   constexpr int CH = 16 * MFC;                                // rows per workgroup
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nl = p.n_local;
+  // offsets[nl] < 0: the dispatch gave up (its outputs are poisoned); then no
+  // expert has rows and the call is flagged
+  {
+    const int last = p.offsets[nl];
+    for (int j = tid; j <= nl; j += NT) s_off[j] = last < 0 ? 0 : p.offsets[j];
+    if (last < 0 && block == 0 && tid == 0 && p.flags != nullptr) atomic_or_1(p.flags, sched::kFlagInput);
+  }
   // chunk table: expert j owns ceil(rows_j / CH) chunks of CH rows.  The
   // grid (sized for the worst case, a multiple of 8 chunks; workgroups past
   // the last chunk return) runs chunk q's column blocks on workgroups
@@ -1409,7 +1462,6 @@ __device__ __forceinline__ void skinny_body(const GemmParams& p, int block, int 
   // chunk's A rows are fetched into one XCD's L2 and shared there by all its
   // column blocks (and in the fused launch GEMM-2 finds act where GEMM-1 of
   // the same chunk wrote it)
-  for (int j = tid; j <= nl; j += NT) s_off[j] = p.offsets[j];
   __syncthreads();
   if (tid < 64) scan_units<CH>(s_off, s_pre, nl, 1);
   __syncthreads();
@@ -1490,13 +1542,15 @@ __device__ __forceinline__ void skinny_body(const GemmParams& p, int block, int 
 #pragma unroll
       for (int f = 0; f < MFC; ++f) cell[f] = p.perm[min(r0 + 16 * f + lr, row_hi - 1)];
     }
-    // thread 0: until the chunk's counter reaches `target` (bounded; a
-    // give-up sets the wait flag and goes on)
+    // thread 0: until the chunk's counter reaches `target` (one more for the
+    // test hook's chunk); a give-up sets the wait flag and *s_gave
     auto wait_count = [&](int target) {
+      if (q == p.dbg_chunk) ++target;
       int polls = 0;
       while (atomic_read(done1) < target) {
-        if (++polls == sched::kWaitLimit) {
+        if (++polls == p.wait_limit) {
           atomic_or_1(sched + sched::kFlags, sched::kFlagWait);
+          *s_gave = 1;
           break;
         }
         __builtin_amdgcn_s_sleep(2);
@@ -1507,7 +1561,10 @@ __device__ __forceinline__ void skinny_body(const GemmParams& p, int block, int 
       // chunk counts once SIG_BLOCKS blocks before the end of its K loop, so
       // GEMM-2's weights do not take memory bandwidth from GEMM-1's until
       // then (the chunk's act is ready when the count is twice the blocks)
-      if (tid == 0) wait_count(n_cb_other);
+      if (tid == 0) {
+        *s_gave = 0;
+        wait_count(n_cb_other);
+      }
       __syncthreads();
       // the weights do not depend on GEMM-1's results: their first DEPTH
       // steps go to registers and the next n_lds steps to LDS before the wait
@@ -1523,9 +1580,12 @@ __device__ __forceinline__ void skinny_body(const GemmParams& p, int block, int 
       }
       if (tid == 0) {
         wait_count(2 * n_cb_other);
+        // the last GEMM-2 workgroup of the chunk past its wait takes out what
+        // every workgroup adds (GEMM-1: two counts each; GEMM-2: one), so a
+        // count that arrives after a give-up still leaves both at zero
         if (atomic_add_1(seen2, 1) == n_cb - 1) {
-          atomicExch(done1, 0);
-          atomicExch(seen2, 0);
+          atomic_add_1(done1, -2 * n_cb_other);
+          atomic_add_1(seen2, -n_cb);
         }
       }
       // this wave's LDS steps have landed (its own lanes read them back)
@@ -1580,6 +1640,16 @@ __device__ __forceinline__ void skinny_body(const GemmParams& p, int block, int 
     for (int f = 0; f < MFC; ++f)
 #pragma unroll
       for (int j = 0; j < 2; ++j) pin_acc(acc[f][j]);
+    // a fused GEMM-2 workgroup whose wait for act gave up stores NaN
+    if constexpr (LDS_STEPS) {
+      if (__builtin_amdgcn_readfirstlane(*s_gave)) {
+        const float nan = __builtin_nanf("");
+#pragma unroll
+        for (int f = 0; f < MFC; ++f)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) acc[f][j] = f32x4{nan, nan, nan, nan};
+      }
+    }
 #pragma unroll
     for (int f = 0; f < MFC; ++f) {
       const int r = r0 + 16 * f + lr;
@@ -1631,20 +1701,26 @@ __device__ __forceinline__ void skinny_body(const GemmParams& p, int block, int 
 // to zero.  Then each thread sums one 16-byte chunk of a token's output row
 // (combine8_chunk: the order of combine8_kernel, so the same bits), reading y
 // with device-scope loads.
-__device__ void skinny_combine(const CombineParams& cp, const uint16_t* y, int cb, int* sched) {
+__device__ void skinny_combine(const CombineParams& cp, const uint16_t* y, int cb, int* sched, int* s_gave) {
   const int tid = threadIdx.x;
   if (tid == 0) {
-    int polls = 0;
-    while (atomic_read(sched + sched::kG2Done) < cp.n_g2) {
-      if (++polls == sched::kWaitLimit) {
+    int polls = 0, gave = 0;
+    const int target = cp.n_g2 + (cb == cp.dbg_comb ? 1 : 0);
+    while (atomic_read(sched + sched::kG2Done) < target) {
+      if (++polls == cp.wait_limit) {
         atomic_or_1(sched + sched::kFlags, sched::kFlagWait);
+        gave = 1;
         break;
       }
       __builtin_amdgcn_s_sleep(2);
     }
+    *s_gave = gave;
+    // the last combine workgroup past its wait takes out what every
+    // workgroup adds, so a GEMM-2 count that arrives after a give-up still
+    // leaves both words at zero
     if (atomic_add_1(sched + sched::kCombDone, 1) == cp.n_comb - 1) {
-      atomicExch(sched + sched::kG2Done, 0);
-      atomicExch(sched + sched::kCombDone, 0);
+      atomic_add_1(sched + sched::kG2Done, -cp.n_g2);
+      atomic_add_1(sched + sched::kCombDone, -cp.n_comb);
     }
   }
   __syncthreads();
@@ -1653,6 +1729,11 @@ __device__ void skinny_combine(const CombineParams& cp, const uint16_t* y, int c
   const int64_t t = q / static_cast<uint32_t>(cpr);
   const int c = static_cast<int>(q - static_cast<uint32_t>(t) * cpr);
   if (t >= cp.n_tokens) return;
+  if (__builtin_amdgcn_readfirstlane(*s_gave)) {             // the wait gave up: NaN outputs
+    const uint32_t nan2 = pack_bf16x2(__builtin_nanf(""), __builtin_nanf(""));
+    *reinterpret_cast<u32x4*>(cp.out + t * cp.hidden + c * 8) = u32x4{nan2, nan2, nan2, nan2};
+    return;
+  }
   combine8_chunk<MEP_DTYPE_BF16>(y, cp.gate, cp.row_of_entry, cp.valid, t, c, cp.hidden, cp.out,
                                  [&](const uint16_t* ptr) {
                                    return load_dev_16(y, cp.y_bytes, static_cast<uint32_t>((ptr - y) * 2));
@@ -1663,7 +1744,7 @@ template <bool GEMM1>
 __global__ __launch_bounds__(skinny::NT) void moe_gemm_skinny_kernel(GemmParams p) {
   __shared__ int s_pre[bfk::NLMAX + 1];                       // chunks before expert j
   __shared__ int s_off[bfk::NLMAX + 1];
-  skinny_body<GEMM1, false>(p, blockIdx.x, 0, nullptr, s_pre, s_off, nullptr);
+  skinny_body<GEMM1, false>(p, blockIdx.x, 0, nullptr, s_pre, s_off, nullptr, nullptr);
 }
 
 // Both small-batch GEMMs in one launch: workgroups [0, g1_blocks) are GEMM-1's,
@@ -1678,10 +1759,12 @@ __global__ __launch_bounds__(skinny::NT) void moe_gemm_skinny_both_kernel(GemmPa
   __shared__ int s_pre[bfk::NLMAX + 1];
   __shared__ int s_off[bfk::NLMAX + 1];
   __shared__ __attribute__((aligned(16))) unsigned char s_w[skinny::LDS_W];
+  __shared__ int s_gave;                                      // a wait of this workgroup gave up
   const int b = blockIdx.x;
-  if (b < g1_blocks) skinny_body<true, true>(p1, b, p2.N / 128, sched, s_pre, s_off, s_w);
-  else if (!COMB || b < g1_blocks + cp.n_g2) skinny_body<false, true, COMB>(p2, b - g1_blocks, p1.N / 64, sched, s_pre, s_off, s_w);
-  else skinny_combine(cp, static_cast<const uint16_t*>(p2.C), b - g1_blocks - cp.n_g2, sched);
+  if (b < g1_blocks) skinny_body<true, true>(p1, b, p2.N / 128, sched, s_pre, s_off, s_w, &s_gave);
+  else if (!COMB || b < g1_blocks + cp.n_g2)
+    skinny_body<false, true, COMB>(p2, b - g1_blocks, p1.N / 64, sched, s_pre, s_off, s_w, &s_gave);
+  else skinny_combine(cp, static_cast<const uint16_t*>(p2.C), b - g1_blocks - cp.n_g2, sched, &s_gave);
 }
 
 // chunks of the small-batch grids: the worst case (each expert adds at most
@@ -1758,7 +1841,18 @@ MoeParams moe_params(const void* x, int64_t n_tokens, int top_k, const int32_t* 
   div_magic(static_cast<uint32_t>(top_k), &p.k_magic, &p.k_shift);
   p.n_queues = queues_for(device_cu_count());
   p.sched = sched;
+  const GiveupTest gt = giveup_test();
+  p.wait_limit = gt.site == MEP_GIVEUP_ROWS ? gt.polls : sched::kWaitLimit;
+  p.dbg_row = gt.site == MEP_GIVEUP_ROWS ? 0 : -1;
   return p;
+}
+
+// The schedule-buffer fields of the small-batch and generic kernels' params.
+void set_sched(GemmParams& g, int32_t* sched) {
+  g.flags = sched != nullptr ? sched + sched::kFlags : nullptr;
+  const GiveupTest gt = giveup_test();
+  g.wait_limit = gt.site == MEP_GIVEUP_CHUNK ? gt.polls : sched::kWaitLimit;
+  g.dbg_chunk = gt.site == MEP_GIVEUP_CHUNK ? 0 : -1;
 }
 
 // The bf16 tiled kernels need K a multiple of 256 (whole four-step rounds,
@@ -1787,6 +1881,7 @@ GemmParams gemm1_params(const void* x, int64_t n_tokens, int top_k, const int32_
   g1.n_tiles_n = inter / (Cfg::BN / 2);
   g1.a_bytes = static_cast<uint32_t>(n_tokens * hidden * dtype_bytes(DT));
   div_magic(static_cast<uint32_t>(top_k), &g1.k_magic, &g1.k_shift);
+  set_sched(g1, nullptr);
   return g1;
 }
 template <int DT, class Cfg>
@@ -1800,6 +1895,7 @@ GemmParams gemm2_params(const void* act, int top_k, const int32_t* perm, const i
   g2.n_tiles_n = hidden / Cfg::BN;
   g2.a_bytes = static_cast<uint32_t>(max_rows * inter * dtype_bytes(DT));
   div_magic(static_cast<uint32_t>(top_k), &g2.k_magic, &g2.k_shift);
+  set_sched(g2, nullptr);
   return g2;
 }
 
@@ -1813,8 +1909,9 @@ int run_gate_up(const void* x, int64_t n_tokens, int top_k, const int32_t* perm,
                                    hidden, inter, act, nullptr, sched);
     e = launch_tiled<kModeGateUp>(p, max_rows, stream);
   } else {
-    const GemmParams g1 = gemm1_params<DT, Cfg>(x, n_tokens, top_k, perm, offsets, n_local, w_in, w_slot, hidden,
-                                                inter, act);
+    GemmParams g1 = gemm1_params<DT, Cfg>(x, n_tokens, top_k, perm, offsets, n_local, w_in, w_slot, hidden,
+                                          inter, act);
+    set_sched(g1, sched);
     if (DT == MEP_DTYPE_BF16) e = launch_skinny<true>(g1, max_rows, stream);
     else e = launch<DT, Cfg, true>(g1, max_rows, stream);
   }
@@ -1832,8 +1929,9 @@ int run_down(const void* act, int top_k, const int32_t* perm, const int32_t* off
                              inter, const_cast<void*>(act), y, sched);
     e = launch_tiled<kModeDown>(p, max_rows, stream);
   } else {
-    const GemmParams g2 = gemm2_params<DT, Cfg>(act, top_k, perm, offsets, n_local, max_rows, w_out, w_slot, hidden,
-                                                inter, y);
+    GemmParams g2 = gemm2_params<DT, Cfg>(act, top_k, perm, offsets, n_local, max_rows, w_out, w_slot, hidden,
+                                          inter, y);
+    set_sched(g2, sched);
     if (DT == MEP_DTYPE_BF16 && inter % 256 == 0) e = launch_skinny<false>(g2, max_rows, stream);
     else e = launch<DT, Cfg, false>(g2, max_rows, stream);
   }
@@ -1965,10 +2063,12 @@ int grouped_impl(const char* fn, const void* x, int64_t n_tokens, int32_t top_k,
     if (rc != MEP_OK) return rc;
     MEP_REQUIRE(aligned16(x) && aligned16(w_in) && aligned16(w_out) && aligned16(workspace) && aligned16(y_entries),
                 MEP_ERR_INVALID_ARG, "%s: buffers must be 16-byte aligned", fn);
-    const GemmParams g1 = gemm1_params<MEP_DTYPE_BF16, CfgBf16>(x, n_tokens, top_k, perm, offsets, n_local, w_in,
-                                                                w_slot, hidden, inter, workspace);
-    const GemmParams g2 = gemm2_params<MEP_DTYPE_BF16, CfgBf16>(workspace, top_k, perm, offsets, n_local, max_rows,
-                                                                w_out, w_slot, hidden, inter, y_entries);
+    GemmParams g1 = gemm1_params<MEP_DTYPE_BF16, CfgBf16>(x, n_tokens, top_k, perm, offsets, n_local, w_in, w_slot,
+                                                          hidden, inter, workspace);
+    GemmParams g2 = gemm2_params<MEP_DTYPE_BF16, CfgBf16>(workspace, top_k, perm, offsets, n_local, max_rows, w_out,
+                                                          w_slot, hidden, inter, y_entries);
+    set_sched(g1, tile_queue);
+    set_sched(g2, tile_queue);
     const hipError_t e = launch_skinny_both(g1, g2, max_rows, tile_queue, comb, static_cast<hipStream_t>(stream));
     MEP_REQUIRE(e == hipSuccess, MEP_ERR_HIP, "%s: %s", fn, hipGetErrorString(e));
     if (combined != nullptr) *combined = comb != nullptr;
@@ -1997,9 +2097,17 @@ extern "C" int mep_experts_check(const int32_t* tile_queue, void* stream) {
   int32_t flags = 0;
   e = hipMemcpy(&flags, tile_queue + mep::sched::kFlags, sizeof(flags), hipMemcpyDeviceToHost);
   MEP_REQUIRE(e == hipSuccess, MEP_ERR_HIP, "mep_experts_check: %s", hipGetErrorString(e));
+  if (flags != 0) {
+    // reported once: the flags are cleared for the launches that follow
+    const int32_t zero = 0;
+    e = hipMemcpy(const_cast<int32_t*>(tile_queue) + mep::sched::kFlags, &zero, sizeof(zero), hipMemcpyHostToDevice);
+    MEP_REQUIRE(e == hipSuccess, MEP_ERR_HIP, "mep_experts_check: %s", hipGetErrorString(e));
+  }
+  MEP_REQUIRE(!(flags & mep::sched::kFlagInput), MEP_ERR_HIP,
+              "mep_experts_check: offsets[n_local] < 0, the dispatch gave up; no tile ran (results invalid)");
   MEP_REQUIRE(!(flags & mep::sched::kFlagWait), MEP_ERR_HIP,
               "mep_experts_check: a workgroup gave up waiting (GEMM-2 for its GEMM-1 rows, or the combine for "
-              "GEMM-2's rows; results invalid)");
+              "GEMM-2's rows; its outputs are NaN)");
   MEP_REQUIRE(!(flags & mep::sched::kFlagDrain), MEP_ERR_HIP,
               "mep_experts_check: a tile queue was not drained (results invalid)");
   return MEP_OK;
@@ -2083,6 +2191,9 @@ extern "C" int mep_grouped_swiglu_combine(const void* x, int64_t n_tokens, int32
     cp.n_tokens = n_tokens;
     cp.hidden = hidden;
     cp.y_bytes = static_cast<uint32_t>(max_rows * hidden * 2);
+    const GiveupTest gt = giveup_test();
+    cp.wait_limit = gt.site == MEP_GIVEUP_COMBINE ? gt.polls : sched::kWaitLimit;
+    cp.dbg_comb = gt.site == MEP_GIVEUP_COMBINE ? 0 : -1;
   }
   bool combined = false;
   int rc = grouped_impl(fn, x, n_tokens, top_k, perm, offsets, n_local, max_rows, w_in, w_out, nullptr, hidden,

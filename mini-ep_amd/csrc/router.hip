@@ -590,9 +590,10 @@ __global__ __launch_bounds__(kWaves * 64) void router32_kernel(const uint16_t* _
 // (counts, flags, table entries: small non-negative values) has a clear top
 // bit, so the workspace must only be zero-filled once before its first use
 // and can then serve calls of any size.  A wait longer than kRowPolls polls sets
-// kFlagBarrier in the block's status word: every workgroup exits, and
-// mep_dispatch_check reports it.
-constexpr int kEpochWord = 32;                    // header word of the epoch (its own 128-byte line)
+// kFlagBarrier in the block's status word: the workgroup places nothing (its
+// entries get kPoisonRow), every workgroup exits, the last one to finish
+// poisons the whole call (finish_exchange) and mep_dispatch_check reports it.
+// The last workgroup to finish also advances the epoch.
 constexpr int kRowPolls = 1 << 20;
 
 struct FusedDispatch {
@@ -605,6 +606,8 @@ struct FusedDispatch {
   uint32_t* header;         // [0] = n_blocks; [kEpochWord]: the epoch
   uint32_t* flags;          // (2 n_blocks,) status words: count pass (0), scatter pass
   const uint8_t* valid;     // (N,) or NULL
+  int polls;                // polls of a row before a workgroup gives up
+  int withhold;             // workgroup that withholds its row (test hook; -1: none)
 };
 
 __device__ __forceinline__ uint32_t load_dev(const uint32_t* p) {
@@ -694,7 +697,7 @@ __global__ __launch_bounds__(kWaves * 64) void route_dispatch32_kernel(const uin
     s_part[part][0][e] = 0;
     s_part[part][1][e] = c;
   } else {
-    if (tid < E) {
+    if (tid < E && b != o.withhold) {
       int c = 0;
 #pragma unroll
       for (int ww = 0; ww < kWaves; ++ww) c += s_wcnt[ww][tid];
@@ -716,7 +719,7 @@ __global__ __launch_bounds__(kWaves * 64) void route_dispatch32_kernel(const uin
 #pragma unroll
         for (int u = 0; u < kBatch; ++u) stale |= (v[u] & ~0xffffffffull) != tag;
         if (!stale) break;
-        if (it >= kRowPolls) { bad = kFlagBarrier; break; }
+        if (it >= o.polls) { bad = kFlagBarrier; break; }
         __builtin_amdgcn_s_sleep(1);
 #pragma unroll
         for (int u = 0; u < kBatch; ++u)
@@ -735,6 +738,9 @@ __global__ __launch_bounds__(kWaves * 64) void route_dispatch32_kernel(const uin
     if (bad) s_flag = bad;
   }
   __syncthreads();
+  // a workgroup whose wait gave up has rows of earlier calls: it places
+  // nothing and leaves route_counts alone
+  const bool gave_up = s_flag != 0u;
   if (tid < E) {
     int pre = 0, tot = 0;
 #pragma unroll
@@ -748,15 +754,17 @@ __global__ __launch_bounds__(kWaves * 64) void route_dispatch32_kernel(const uin
     const int off = incl - tot;
     s_base[tid] = off + pre;
     if (b == 0) {
+      // device scope, as is the poison that may replace offsets[E]
       o.counts[tid] = tot;
-      o.offsets[tid] = off;
-      if (tid == E - 1) o.offsets[E] = incl;
-      if (o.route_counts != nullptr) o.route_counts[tid] += tot;
+      store_dev(reinterpret_cast<uint32_t*>(o.offsets + tid), static_cast<uint32_t>(off));
+      if (tid == E - 1) store_dev(reinterpret_cast<uint32_t*>(o.offsets + E), static_cast<uint32_t>(incl));
+      if (o.route_counts != nullptr && !gave_up) o.route_counts[tid] += tot;
     }
   }
   __syncthreads();
 
-  // 3. rows of this lane's entries
+  // 3. rows of this lane's entries (row_of_entry with device-scope stores,
+  // as is the poison that may replace it)
   const int t = lane >> 2, g = lane & 3;
   if (t0 + t < n_tokens) {
     const int64_t f = (t0 + t) * KC + g * 2;
@@ -764,8 +772,8 @@ __global__ __launch_bounds__(kWaves * 64) void route_dispatch32_kernel(const uin
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int e = sel[h];
-      row[h] = -1;
-      if (e >= 0) {
+      row[h] = gave_up ? kPoisonRow : -1;
+      if (e >= 0 && !gave_up) {
         int r = s_base[e] + rank[h];
 #pragma unroll
         for (int ww = 0; ww < kWaves; ++ww) r += ww < wave ? s_wcnt[ww][e] : 0;
@@ -773,16 +781,22 @@ __global__ __launch_bounds__(kWaves * 64) void route_dispatch32_kernel(const uin
         o.perm[r] = static_cast<int32_t>(f + h);
       }
     }
-    o.row_of_entry[f] = row[0];
-    o.row_of_entry[f + 1] = row[1];
+    store_dev(reinterpret_cast<uint64_t*>(o.row_of_entry + f),
+              (static_cast<uint64_t>(static_cast<uint32_t>(row[1])) << 32) | static_cast<uint32_t>(row[0]));
   }
   if (tid == 0) {
     o.flags[b] = 0u;
     o.flags[nb + b] = s_flag;
-    if (b == 0) {
-      o.header[0] = static_cast<uint32_t>(nb);
-      // every row of this call has been seen, so every workgroup has read the epoch
-      if (nb > 1) store_dev(o.header + kEpochWord, epoch);
+    if (b == 0) o.header[0] = static_cast<uint32_t>(nb);
+  }
+  if (nb > 1) {
+    // the last workgroup to finish poisons a call in which one gave up, and
+    // advances the epoch (every workgroup has read it)
+    __syncthreads();
+    if (tid < 64) {
+      const int r = finish_exchange(o.header, gave_up, nb);
+      if (r & kExchangeGaveUp) poison_dispatch(o.row_of_entry, n_tokens * KC, o.offsets, E);
+      if ((r & kExchangeLast) && tid == 0) store_dev(o.header + kEpochWord, epoch);
     }
   }
 }
@@ -888,7 +902,10 @@ hipError_t launch_route_dispatch_fused(const void* x, const void* w, int64_t n, 
   if (dtype != MEP_DTYPE_BF16 || E != 32 || k != 8 || n_blocks < 1 ||
       static_cast<int64_t>(n_blocks) * kWaves * kRowsPerWave < n)
     return hipErrorNotSupported;
-  const FusedDispatch o{counts, offsets, perm, row_of_entry, route_counts, rows, header, flags, valid};
+  const GiveupTest gt = giveup_test();
+  const bool test = gt.site == MEP_GIVEUP_DISPATCH;
+  const FusedDispatch o{counts, offsets, perm, row_of_entry, route_counts, rows, header, flags, valid,
+                        test ? gt.polls : kRowPolls, test ? n_blocks - 1 : -1};
   const uint16_t* xb = static_cast<const uint16_t*>(x);
   const uint16_t* wb = static_cast<const uint16_t*>(w);
   uint16_t* gb = static_cast<uint16_t*>(gate);

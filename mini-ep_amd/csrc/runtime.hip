@@ -37,8 +37,25 @@ int device_cu_count() {
   return n;
 }
 
+static std::atomic<int> g_giveup_site{0}, g_giveup_polls{0};
+
+GiveupTest giveup_test() {
+  return GiveupTest{g_giveup_site.load(std::memory_order_relaxed), g_giveup_polls.load(std::memory_order_relaxed)};
+}
+
 }  // namespace mep
+
+extern "C" int mep_test_force_giveup(int32_t site, int32_t polls) {
+  mep::clear_error();
+  MEP_REQUIRE(site >= MEP_GIVEUP_NONE && site <= MEP_GIVEUP_COMBINE, MEP_ERR_INVALID_ARG,
+              "mep_test_force_giveup: unknown site %d", site);
+  MEP_REQUIRE(site == MEP_GIVEUP_NONE || polls > 0, MEP_ERR_INVALID_ARG,
+              "mep_test_force_giveup: polls must be positive (got %d)", polls);
+  mep::g_giveup_polls.store(site == MEP_GIVEUP_NONE ? 0 : polls, std::memory_order_relaxed);
+  mep::g_giveup_site.store(site, std::memory_order_relaxed);
+  return MEP_OK;
+}
 
 extern "C" const char* mep_last_error(void) { return mep::g_last_error; }
 
-extern "C" int mep_abi_version(void) { return 4; }
+extern "C" int mep_abi_version(void) { return 5; }

@@ -26,6 +26,14 @@ ERR_HIP = -6
 DISPATCH_STATUS_RANGE = 1
 DISPATCH_STATUS_NOT_RESIDENT = 2
 DISPATCH_STATUS_REPLICAS = 4
+DISPATCH_STATUS_BARRIER = 8
+
+# sites of the give-up test hook (mep_test_force_giveup)
+GIVEUP_NONE = 0
+GIVEUP_DISPATCH = 1
+GIVEUP_ROWS = 2
+GIVEUP_CHUNK = 3
+GIVEUP_COMBINE = 4
 
 
 class MepError(RuntimeError):
@@ -100,6 +108,7 @@ _SIGNATURES = {
                                        _c_void_p, _c_void_p, _c_void_p]),
     "mep_combine_rows": (ctypes.c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i32,
                                         _i32, _i32, _c_void_p, _c_void_p]),
+    "mep_test_force_giveup": (ctypes.c_int, [_i32, _i32]),
 }
 
 _LIB = None

@@ -41,11 +41,12 @@ class HipMoEBackend:
     """All experts resident on this GPU: LocalMoEBackend (modeling.py:131-145).
 
     w_in (E, 2I, H), w_out (E, H, I) device tensors in the compute dtype.
-    ``check`` synchronises after dispatch to raise on out-of-range expert ids
-    (the reference raises when it indexes w_in); switch it off in serving
-    loops that must not sync."""
+    ``check=True`` synchronises after the dispatch and again after the
+    experts: it raises on out-of-range expert ids (the reference raises when
+    it indexes w_in) and on a kernel wait that gave up (whose outputs are
+    NaN).  Off by default, so that a call never synchronises the host."""
 
-    def __init__(self, w_in: torch.Tensor, w_out: torch.Tensor, check: bool = True):
+    def __init__(self, w_in: torch.Tensor, w_out: torch.Tensor, check: bool = False):
         if not w_in.is_cuda or not w_out.is_cuda:
             raise RuntimeError("HipMoEBackend needs device-resident expert weights")
         self.w_in = w_in.contiguous()
@@ -59,8 +60,11 @@ class HipMoEBackend:
         disp = ops.dispatch(topk_idx, valid_mask, self.num_experts, self._table, self._n_rep,
                             False, None, 0, self._g2l, self.num_experts, check=self.check)
         self.last_dispatch = disp
-        return ops.grouped_swiglu_combine(x_flat.to(self.w_in.dtype), disp, self.w_in, self.w_out, topk_gate,
-                                          valid_mask)
+        out = ops.grouped_swiglu_combine(x_flat.to(self.w_in.dtype), disp, self.w_in, self.w_out, topk_gate,
+                                         valid_mask)
+        if self.check:
+            ops.experts_check(out.device)
+        return out
 
     def route_and_call(self, x_flat, w_router, k, valid_mask=None):
         """The router hook and this backend in one go (Block.forward,
@@ -70,7 +74,10 @@ class HipMoEBackend:
         x = x_flat.to(self.w_in.dtype)
         idx, gate, disp = ops.route_dispatch(x, w_router, k, valid_mask, check=self.check)
         self.last_dispatch = disp
-        return ops.grouped_swiglu_combine(x, disp, self.w_in, self.w_out, gate, valid_mask), idx, gate
+        out = ops.grouped_swiglu_combine(x, disp, self.w_in, self.w_out, gate, valid_mask)
+        if self.check:
+            ops.experts_check(out.device)
+        return out, idx, gate
 
 
 class EPStats:

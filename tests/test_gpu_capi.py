@@ -107,4 +107,4 @@ def test_error_codes_and_messages():
                               big.data_ptr(), 1024, 512, 1, big.data_ptr(), big.data_ptr(), big.numel() * 4,
                               None, need, None)
     assert rc == _lib.ERR_INVALID_ARG
-    assert L.mep_abi_version() == 4
+    assert L.mep_abi_version() == 5

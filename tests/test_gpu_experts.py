@@ -160,6 +160,49 @@ def _two_launches(x, d, w_in, w_out, y):
     return ops.swiglu_down(act, x, d, w_out, y)
 
 
+def test_one_launch_consecutive_inputs_same_buffers():
+    """The tiled one launch hands act from GEMM-1 tiles to GEMM-2 tiles that
+    may run on other XCDs (device-scope act stores, GEMM-2 reads of lines its
+    XCD has not cached in this launch).  Different inputs and routings, run
+    back to back through the same act workspace, y buffer and schedule words
+    (A, B, A, B), must each give the two launches' bits: an act line left over
+    from the previous call would show here, where a repeated identical input
+    would not."""
+    banner("experts one launch: consecutive inputs through the same buffers")
+    from miniep_amd import _lib
+    bf = torch.bfloat16
+    Lib = _lib.lib()
+    n, k = 8192, 8
+    cases = []
+    for i in range(2):
+        L = workloads.make_layer(n, seed=51 + i, zipf_s=1.2 if i == 0 else 0.6)
+        topk = (L.x @ L.w_router.T).topk(k, dim=-1).indices
+        E = L.w_in.shape[0]
+        table, n_rep, g2l = _world1(E)
+        d = ops.dispatch(topk.to(DEV), None, E, table, n_rep, False, None, 0, g2l, E)
+        x, wi, wo = L.x.to(bf).to(DEV), L.w_in.to(bf).to(DEV), L.w_out.to(bf).to(DEV)
+        ref = torch.full((n * k, 1024), 7.0, dtype=bf, device=DEV)
+        _two_launches(x, d, wi, wo, ref)
+        cases.append((x, d, wi, wo, ref))
+    assert not torch.equal(cases[0][1].perm, cases[1][1].perm)
+    max_rows = n * k
+    ws = torch.empty(int(Lib.mep_experts_workspace_size(max_rows, 512, _lib.DTYPE_BF16)), dtype=torch.uint8,
+                     device=DEV)
+    tq = torch.zeros(int(Lib.mep_experts_queue_ints(max_rows, 32)), dtype=torch.int32, device=DEV)
+    y = torch.empty((n * k, 1024), dtype=bf, device=DEV)
+    st = torch.cuda.current_stream().cuda_stream
+    for rep in range(4):
+        x, d, wi, wo, ref = cases[rep % 2]
+        y.fill_(7.0)
+        rc = Lib.mep_grouped_swiglu(x.data_ptr(), n, k, d.perm.data_ptr(), d.offsets.data_ptr(), 32, max_rows,
+                                    wi.data_ptr(), wo.data_ptr(), 1024, 512, _lib.DTYPE_BF16, y.data_ptr(),
+                                    ws.data_ptr(), ws.numel(), tq.data_ptr(), tq.numel(), st)
+        assert rc == 0
+        _lib.check(Lib.mep_experts_check(tq.data_ptr(), st), "mep_experts_check")
+        assert torch.equal(y, ref), rep
+        assert int(tq.abs().sum()) == 0
+
+
 @pytest.mark.parametrize("case", ["zipf_t16384", "tiny_t300", "ragged_e16", "e64_masked", "zipf_t40000"])
 def test_one_launch_equals_two_launches(case):
     """bf16 with more than 2048 entries runs both GEMMs as one launch (each

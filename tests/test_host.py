@@ -19,10 +19,10 @@ from oracle import moe_oracle as O
 def test_library_exports_every_header_function():
     L = _lib.lib()
     names = _lib.header_functions()
-    assert len(names) == 22
+    assert len(names) == 23
     for n in names:
         assert hasattr(L, n), n
-    assert L.mep_abi_version() == 4
+    assert L.mep_abi_version() == 5
     assert _lib.last_error() == ""
 
 
