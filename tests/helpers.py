@@ -19,6 +19,15 @@ def rel_err(got, ref) -> float:
     return float(np.abs(got - ref).max() / scale)
 
 
+def row_rel_err(got, ref, floor: float) -> float:
+    """Largest per-row error: max over rows of max|got - ref| / max(max|ref row|, floor).
+    Catches a row that is wrong by much less than the largest row of the tensor."""
+    got = np.asarray(got, np.float64).reshape(len(got), -1)
+    ref = np.asarray(ref, np.float64).reshape(len(ref), -1)
+    scale = np.maximum(np.abs(ref).max(axis=1), floor)
+    return float((np.abs(got - ref).max(axis=1) / scale).max())
+
+
 def to_np(t: torch.Tensor) -> np.ndarray:
     """Device tensor -> numpy (bf16 widened to its exact float32 values)."""
     t = t.detach()

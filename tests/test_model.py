@@ -68,3 +68,43 @@ def test_config_from_reference_field_names(tmp_path):
     p.write_text(json.dumps(raw))
     cfg = ModelConfig.from_json(p)
     assert cfg == TINY and cfg.head_dim == 16
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_torch_moe_ref_pinned_against_oracle(dtype):
+    """TorchMoERef and torch_route, the reference MoE block of the full-model
+    tests, against the numpy oracle (router_logits + topk_softmax,
+    moe_layer_local) on tie-free rows with masked tokens, fp32 (bar 1e-5) and
+    bf16 (act and expert outputs rounded to bf16; bar 2e-2 normwise and per
+    row).  A planted mutant -- gate and up halves swapped -- must fail the bar."""
+    import numpy as np
+
+    from helpers import TOL_BF16, TOL_F32, rel_err, row_rel_err, tie_free
+    from oracle import moe_oracle as O
+
+    g = torch.Generator().manual_seed(7)
+    n, H, inter, E, k = 96, 128, 64, 8, 2
+    x = torch.randn(n, H, generator=g).to(dtype)
+    w_r = (torch.randn(E, H, generator=g) * 0.1).to(dtype)
+    w_in = (torch.randn(E, 2 * inter, H, generator=g) * 0.05).to(dtype)
+    w_out = (torch.randn(E, H, inter, generator=g) * 0.05).to(dtype)
+    valid = torch.rand(n, generator=g) < 0.8
+    bf = dtype == torch.bfloat16
+    xf, wrf, wif, wof = (t.float().numpy() for t in (x, w_r, w_in, w_out))
+
+    idx, gate = torch_route(x, w_r, k)
+    lg = O.router_logits(xf, wrf)
+    assert tie_free(lg, k)
+    oidx, ogate = O.topk_softmax(lg, k, gate_bf16=bf)
+    assert np.array_equal(idx.numpy(), oidx)
+    np.testing.assert_allclose(gate.float().numpy(), ogate, rtol=1e-2 if bf else 1e-6, atol=0)
+
+    want = O.moe_layer_local(xf, oidx, gate.float().numpy(), wif, wof, valid.numpy(), act_bf16=bf, out_bf16=bf)
+    got = TorchMoERef(w_in, w_out)(x, idx, gate, valid).float().numpy()
+    tol = TOL_BF16 if bf else TOL_F32
+    assert (got[~valid.numpy()] == 0).all()
+    assert rel_err(got, want) <= tol
+    assert row_rel_err(got[valid.numpy()], want[valid.numpy()], floor=1e-3 * float(np.abs(want).max())) <= tol
+    swapped = torch.cat([w_in[:, inter:], w_in[:, :inter]], dim=1)
+    bad = TorchMoERef(swapped, w_out)(x, idx, gate, valid).float().numpy()
+    assert rel_err(bad, want) > 10 * tol
