@@ -62,9 +62,9 @@ def test_live_replacement_copies_only_arriving_experts(golden_dir):
     balanced = Placement.from_plan(plan, device=DEV)
     naive = Placement.naive(24, 32, 4, device=DEV)
     g = torch.Generator().manual_seed(21)
-    ck_in = [(torch.randn(32, 1024, 1024, generator=g) * 0.02).to(BF).to(DEV) for _ in range(24)]
-    ck_out = [(torch.randn(32, 1024, 512, generator=g) * 0.02).to(BF).to(DEV) for _ in range(24)]
-    checkpoint = lambda l: (ck_in[l], ck_out[l])
+    ck_in = (torch.randn(24, 32, 1024, 1024, generator=g) * 0.02).to(BF).to(DEV)
+    ck_out = (torch.randn(24, 32, 1024, 512, generator=g) * 0.02).to(BF).to(DEV)
+    checkpoint = (ck_in, ck_out)                 # all layers in one launch per rank
     stores = [ExpertStore(24, 10, 1024, 512, BF, DEV) for _ in range(4)]
     for r, st in enumerate(stores):
         for l in range(24):
@@ -91,7 +91,9 @@ def test_live_replacement_copies_only_arriving_experts(golden_dir):
           f"{1e3 * secs:.2f} ms over 4 ranks x 24 layers", flush=True)
     assert copied == replicas == 71
     check_all_layers(balanced)
-    back = sum(apply_placement([], st, naive, r, checkpoint)["copied"] for r, st in enumerate(stores))
+    # back to the naive placement, one layer per launch this time (the callable checkpoint)
+    back = sum(apply_placement([], st, naive, r, lambda l: (ck_in[l], ck_out[l]))["copied"]
+               for r, st in enumerate(stores))
     assert back == 0                              # the owned experts never left their slots
     check_all_layers(naive)
 
