@@ -352,6 +352,31 @@ int mep_combine_rows(const void* y_rows, const void* topk_gate, const int32_t* r
                      int32_t hidden, int32_t dtype, void* out, void* stream);
 
 /* ------------------------------------------------------------------------
+ * The whole MoE block of the all-local backend for one batch: the router
+ * hook and the backend call of Block.forward (modeling.py:192-196), i.e.
+ * mep_route_dispatch followed by mep_grouped_swiglu_combine, with the outputs
+ * of both (topk_idx, topk_gate, logits if non-NULL, counts, offsets, perm,
+ * row_of_entry, route_counts += if non-NULL, y_entries, out) bit for bit.
+ * Decode batches of GraniteMoE's shape (bf16, 32 experts, top-8, 1..32
+ * tokens, hidden 1024 / 2048 / 4096, inter % 256 == 0) run as ONE launch:
+ * one workgroup routes while the expert workgroups already stream their
+ * weights, and the last GEMM-2 workgroup of each column block combines it
+ * (tile_queue_ints >= mep_moe_layer_queue_ints(...) words, zero before the
+ * first call; mep_experts_check reports a wait that gave up).  Other shapes
+ * make the two calls.  Workspaces: dispatch_ws as mep_route_dispatch's
+ * (zero-filled once), experts_ws as mep_grouped_swiglu's.
+ * ---------------------------------------------------------------------- */
+size_t mep_moe_layer_queue_ints(int64_t n_tokens, int32_t n_experts, int32_t hidden);
+
+int mep_moe_layer(const void* x, const void* w_router, const uint8_t* valid_mask, int64_t n_tokens,
+                  int32_t hidden, int32_t n_experts, int32_t top_k, int32_t dtype, const void* w_in,
+                  const void* w_out, int32_t inter, int64_t* topk_idx, void* topk_gate, float* logits,
+                  int32_t* counts, int32_t* offsets, int32_t* perm, int32_t* row_of_entry,
+                  int64_t* route_counts, void* y_entries, void* dispatch_ws, size_t dispatch_ws_bytes,
+                  void* experts_ws, size_t experts_ws_bytes, int32_t* tile_queue, size_t tile_queue_ints,
+                  void* out, void* stream);
+
+/* ------------------------------------------------------------------------
  * Test hook, no counterpart in the reference: makes one of the bounded waits
  * of the one-launch kernels give up, so that tests can drive the give-up
  * path from the host (every wait still ends, every kernel exits).  While a
@@ -365,7 +390,12 @@ int mep_combine_rows(const void* y_rows, const void* topk_gate, const int32_t* r
  *                        launch wait for one GEMM-1 count more than exists;
  *   MEP_GIVEUP_COMBINE   combine workgroup 0 of the small-batch launch that
  *                        ends with the combine waits for one GEMM-2
- *                        workgroup more than exists.
+ *                        workgroup more than exists;
+ *   MEP_GIVEUP_ROUTED    the first GEMM workgroup of mep_moe_layer's one
+ *                        launch waits for the routing to be counted twice
+ *                        (its give-up makes every output of the call NaN);
+ *                        MEP_GIVEUP_CHUNK applies to that launch too (the
+ *                        GEMM-2 workgroups of expert 0).
  * A give-up is reported as in normal operation (mep_dispatch_check,
  * mep_experts_check) and poisons what the caller consumes: a dispatch sets
  * offsets[n_local] = -1 and every row_of_entry to -2 (the experts kernels then
@@ -379,6 +409,7 @@ int mep_combine_rows(const void* y_rows, const void* topk_gate, const int32_t* r
 #define MEP_GIVEUP_ROWS 2
 #define MEP_GIVEUP_CHUNK 3
 #define MEP_GIVEUP_COMBINE 4
+#define MEP_GIVEUP_ROUTED 5
 int mep_test_force_giveup(int32_t site, int32_t polls);
 
 #ifdef __cplusplus

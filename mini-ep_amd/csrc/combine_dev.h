@@ -34,7 +34,9 @@ __device__ __forceinline__ u32x4 pack_row_chunk(const float* acc) {
   return o;
 }
 
-template <int DT, class LoadY>
+// DEV: the token's row_of_entry entries and gates are read with device-scope
+// loads (written earlier in the same launch, possibly on another XCD).
+template <int DT, class LoadY, bool DEV = false>
 __device__ __forceinline__ void combine8_chunk(const typename Elem<DT>::T* __restrict__ y,
                                                const typename Elem<DT>::T* __restrict__ gate,
                                                const int32_t* __restrict__ row_of_entry,
@@ -49,10 +51,28 @@ __device__ __forceinline__ void combine8_chunk(const typename Elem<DT>::T* __res
   for (int s = 0; s < K; ++s) v[s] = load_y(ybase + static_cast<int64_t>(s) * hidden);
   int32_t row[K];
   float g[K];
+  if constexpr (DEV) {
+    static_assert(DT == MEP_DTYPE_BF16, "device-scope reads of bf16 gates");
+    const uint64_t* rp = reinterpret_cast<const uint64_t*>(row_of_entry + t * K);
+    const uint64_t* gp = reinterpret_cast<const uint64_t*>(gate + t * K);
 #pragma unroll
-  for (int s = 0; s < K; ++s) {
-    row[s] = row_of_entry[t * K + s];
-    g[s] = Elem<DT>::to_f32(gate[t * K + s]);
+    for (int h = 0; h < K / 2; ++h) {
+      const uint64_t v = __hip_atomic_load(rp + h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      row[2 * h] = static_cast<int32_t>(static_cast<uint32_t>(v));
+      row[2 * h + 1] = static_cast<int32_t>(static_cast<uint32_t>(v >> 32));
+    }
+#pragma unroll
+    for (int h = 0; h < K / 4; ++h) {
+      const uint64_t v = __hip_atomic_load(gp + h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) g[4 * h + q] = bf16_to_f32(static_cast<uint16_t>(v >> (16 * q)));
+    }
+  } else {
+#pragma unroll
+    for (int s = 0; s < K; ++s) {
+      row[s] = row_of_entry[t * K + s];
+      g[s] = Elem<DT>::to_f32(gate[t * K + s]);
+    }
   }
   const bool tok_ok = valid == nullptr || valid[t] != 0;
   bool poison = false;

@@ -45,6 +45,7 @@
 // path walks K in the same order, so they give the same bits.
 #include "combine_dev.h"
 #include "common.h"
+#include "router_dev.h"
 
 #include <type_traits>
 
@@ -1393,6 +1394,42 @@ constexpr int LDS_W = NW * LSTEPS * 2 * 1024;
 // tiled kernel: GEMM-1 between 1024 and 2048 entries, GEMM-2 past 2048)
 constexpr int64_t kMaxEntries1 = 1024, kMaxEntries2 = 2048;
 static_assert(kMaxEntries1 == sched::kSmallRows, "schedule words of the small-batch launch");
+static_assert(LSTEPS == DEPTH, "the K loop's first block reads all the LDS steps");
+
+// The K loop of a small-batch workgroup with DEPTH K-steps of loads in
+// flight (KT steps, a multiple of DEPTH; the caller has loaded block 0):
+// block b of DEPTH steps runs its MFMAs and issues block b + 1's loads --
+// block 1's with `first` (from LDS where the caller staged them), the later
+// ones with `next` -- and the last block runs only its MFMAs.  No load sits
+// under a run-time condition inside a block: the compiler then counts the
+// loads in flight exactly and each step waits only for its own operands.  (A
+// conditional load makes it wait for every load in flight at the end of each
+// block, and the pipeline drains every DEPTH steps: the loop then runs at
+// one memory latency per block.)  Block 1 is peeled too, so that the loop
+// is entered with the loads in flight that it has at every iteration and
+// its waits are the steady state's.  at_block(b) runs before block b.
+template <class Mfma, class First, class Next, class AtBlock>
+__device__ __forceinline__ void k_pipeline(int KT, Mfma mfma, First first, Next next, AtBlock at_block) {
+  const int NB = KT / DEPTH;
+  auto block = [&](int b, auto load) {
+    at_block(b);
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      mfma(d);
+      load((b + 1) * DEPTH + d, d);
+    }
+  };
+  if (NB > 1) {
+    block(0, first);
+    if (NB > 2) {
+      block(1, next);
+      for (int b = 2; b < NB - 1; ++b) block(b, next);
+    }
+  }
+  at_block(NB - 1);
+#pragma unroll
+  for (int d = 0; d < DEPTH; ++d) mfma(d);
+}
 }  // namespace skinny
 
 // The combine that ends a small-batch launch (moe_gemm_skinny_both_kernel
@@ -1519,15 +1556,14 @@ __device__ __forceinline__ void skinny_body(const GemmParams& p, int block, int 
     const int n_lds = LDS_STEPS ? min(LSTEPS, KT - DEPTH) : 0;
     unsigned char* const w_lds = LDS_STEPS ? s_w + wave * (LSTEPS * 2 * 1024) : nullptr;
     auto load_w = [&](int t, int slot) {
-      if (LDS_STEPS && t >= DEPTH && t < DEPTH + n_lds) {
-        const unsigned char* b = w_lds + (t - DEPTH) * 2048 + 16 * lane;
-        wq[slot][0] = *reinterpret_cast<const u32x4*>(b);
-        wq[slot][1] = *reinterpret_cast<const u32x4*>(b + 1024);
-        return;
-      }
       const int64_t off = k_off(t);
       wq[slot][0] = *reinterpret_cast<const u32x4*>(wp0 + off);
       wq[slot][1] = *reinterpret_cast<const u32x4*>(wp1 + off);
+    };
+    auto load_w_lds = [&](int t, int slot) {             // a step staged in LDS: [DEPTH, DEPTH + n_lds)
+      const unsigned char* b = w_lds + (t - DEPTH) * 2048 + 16 * lane;
+      wq[slot][0] = *reinterpret_cast<const u32x4*>(b);
+      wq[slot][1] = *reinterpret_cast<const u32x4*>(b + 1024);
     };
     if constexpr (!LDS_STEPS) {
       // the weights need only the chunk's expert: their first steps go out
@@ -1616,23 +1652,28 @@ __device__ __forceinline__ void skinny_body(const GemmParams& p, int block, int 
       for (int j = 0; j < 2; ++j) acc[f][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) load_a(d, d);
-    for (int t0 = 0; t0 < KT; t0 += DEPTH) {             // KT is a multiple of DEPTH
-      // fused GEMM-1: the first count of the chunk, SIG_BLOCKS blocks of
-      // DEPTH steps before the end of the K loop (at its start when shorter)
-      if (FUSED && GEMM1 && t0 == (KT > SIG_BLOCKS * DEPTH ? KT - SIG_BLOCKS * DEPTH : 0) && tid == 0)
-        atomic_add_1(done1, 1);
+    auto mfma_step = [&](int d) {
 #pragma unroll
-      for (int d = 0; d < DEPTH; ++d) {
+      for (int f = 0; f < MFC; ++f)
 #pragma unroll
-        for (int f = 0; f < MFC; ++f)
-#pragma unroll
-          for (int j = 0; j < 2; ++j) mfma_acc(acc[f][j], wq[d][j], aq[d][f]);
-        if (t0 + d + DEPTH < KT) {
-          load_w(t0 + d + DEPTH, d);
-          load_a(t0 + d + DEPTH, d);
-        }
-      }
-    }
+        for (int j = 0; j < 2; ++j) mfma_acc(acc[f][j], wq[d][j], aq[d][f]);
+    };
+    auto next = [&](int t, int slot) {
+      load_w(t, slot);
+      load_a(t, slot);
+    };
+    auto first = [&](int t, int slot) {
+      if constexpr (LDS_STEPS) load_w_lds(t, slot);
+      else load_w(t, slot);
+      load_a(t, slot);
+    };
+    // fused GEMM-1: the first count of the chunk, SIG_BLOCKS blocks of DEPTH
+    // steps before the end of the K loop (at its start when shorter)
+    const int nb = KT / DEPTH, b_sig = nb > SIG_BLOCKS ? nb - SIG_BLOCKS : 0;
+    auto at_block = [&](int b) {
+      if (FUSED && GEMM1 && b == b_sig && tid == 0) atomic_add_1(done1, 1);
+    };
+    k_pipeline(KT, mfma_step, first, next, at_block);
     // results: lane (lr, lg) of fragment j holds columns 4 lg .. 4 lg + 3 of
     // the fragment for row lr of each row fragment
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
@@ -1803,6 +1844,552 @@ hipError_t launch_skinny_both(const GemmParams& p1, const GemmParams& p2, int64_
         p1, p2, static_cast<int>(b1), sched, cp);
   }
   return hipGetLastError();
+}
+
+// ============================================================================
+// The decode layer in one launch (mep_moe_layer): router + dispatch, GEMM-1 +
+// SwiGLU, GEMM-2 and the combine, for bf16, 32 experts, top-8 and at most 32
+// tokens (every expert then has at most one 32-row chunk).
+//
+// Workgroup 0 routes the batch (router + one-block dispatch, the same
+// instructions as mep_route_dispatch's one-workgroup path, so the same bits),
+// stores everything, writes its XCD's L2 back to memory (release at device
+// scope) and then publishes one routing record per expert: a 64-bit word
+// (written once, so read whole) holding a written bit, the expert's first
+// row and its tokens as a bit mask.  Workgroups are dispatched in grid
+// order, so it is resident before anyone waits for it.  The GEMM workgroups
+// that follow are expert-major: (expert e, column block cb), all column
+// blocks of expert e on XCD (e + 1) mod 8 for both GEMMs (act stays in one
+// L2).  GEMM-1 does not wait for the routing: a batch has at most 32 tokens,
+// one MFMA row block, so each GEMM-1 workgroup computes its expert's
+// gate/up columns for every token while workgroup 0 routes -- the weight
+// stream, not the MFMAs, sets its time, and that stream is the same -- and
+// then reads its expert's record (one load, issued before its last block of
+// K-steps; the routing is done by then) to store the act rows of the tokens
+// routed to e: token t's row is the first row plus the routed tokens before
+// t (the block lists its entries in token order).  A row's MFMA result
+// depends only on that row, in the same K order and with the same MFMAs as
+// skinny_body, so act has the two-call path's bits.  Each GEMM-1 workgroup
+// then adds 2 to its expert's count; the last of workgroup 0 and the GEMM-1
+// workgroups to finish clears the records for the next launch.  GEMM-2
+// workgroups stream their weights (all of K = 512: registers + LDS) up
+// front, wait only for that count to reach twice the GEMM-1 column blocks,
+// then read the rows (written before the records) and act.  The combine has
+// no wait of its own: the last GEMM-2 workgroup of a column block to finish
+// (one per expert with rows) combines that column block for every token
+// (combine8_chunk, the same slot-order sum as mep_combine), reading y, the
+// gates and row_of_entry with device-scope loads.  A wait that gives up sets
+// the wait flag; the routing wait also poisons the launch (schedule word
+// dec::kPoison: every output NaN); every counter is taken back out by the
+// last workgroup that uses it.
+namespace dec {
+constexpr int kMaxTokens = 32;
+constexpr int E = 32;
+constexpr int kSeen = 15;                               // workgroups done with the routing records
+constexpr int kExpert = sched::kRowDone;                // [16, 16 + 2E): per expert GEMM-1 counts, GEMM-2 readers
+constexpr int kPoison = sched::kRowDone + 2 * E;        // a routing wait gave up
+constexpr int kCombined = kPoison + 1;                  // column blocks combined
+constexpr int kCol = kCombined + 1;                     // [.., + H / 128): GEMM-2 workgroups done per column block
+// [kRec(H), + 2E): the routing record of each expert, one 64-bit word:
+// bit 63 set once written, bits 32..47 the expert's first row, bits 0..31
+// its tokens (bit t: token t is routed to the expert)
+inline int kRec(int hidden) { return (kCol + hidden / 128 + 1) & ~1; }
+constexpr uint64_t kRecValid = 1ull << 63;
+constexpr int kRouterLds = E * kRowStride32 + kWaves * kRowsPerWave * (E + 1) * 4 + kWaves * E * 4 + 2 * E * 4;
+constexpr int kLds = kRouterLds > skinny::LDS_W ? kRouterLds : skinny::LDS_W;
+inline int64_t words(int hidden) { return kRec(hidden) + 2 * E; }
+}  // namespace dec
+
+struct DecodeParams {
+  const uint16_t* x;             // (n, H)
+  const uint16_t* w_router;      // (E, H)
+  const uint8_t* valid;          // (n,) or NULL
+  int64_t n_tokens;
+  int64_t* topk_idx;             // (n, 8)
+  uint16_t* gate;                // (n, 8)
+  float* logits;                 // (n, E) or NULL
+  int32_t* counts;               // (E,)
+  int32_t* offsets;              // (E + 1,)
+  int32_t* perm;                 // (n * 8,)
+  int32_t* row_of_entry;         // (n * 8,)
+  int64_t* route_counts;         // (E,) or NULL
+  uint32_t* ws_header;           // dispatch workspace: header word 0 and the two status words
+  uint32_t* ws_flags;
+  GemmParams g1, g2;             // GEMM-1: x -> act; GEMM-2: act -> y_entries
+  uint16_t* out;                 // (n, H)
+  int n_g1, n_g2;                // GEMM-1 / GEMM-2 workgroups (E x column blocks each)
+  int* sched;
+  int wait_limit;                // polls before GEMM-2's wait for act gives up
+  int route_wait_limit;          // polls before GEMM-1's wait for its routing record gives up
+  int dbg_routed;                // GEMM-1 workgroup whose routing wait cannot end (test hook; -1: none)
+  uint64_t* rec;                 // the routing records (in sched)
+};
+
+// Device-scope 32-bit load (written earlier in this launch, possibly on another XCD).
+__device__ __forceinline__ int load_dev_i32(const int32_t* q) {
+  return __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Workgroup 0: route the batch (router32_logits, router_tail: the fused
+// router's code), dispatch it as one block (flat order, stable by expert:
+// modeling.py:94-96), then publish the routing.
+template <int NSEG>
+__device__ void decode_route(const DecodeParams& p, unsigned char* lds) {
+  constexpr int E = dec::E, KC = 8;
+  unsigned char* const ws = lds;
+  float (*lg)[kRowsPerWave][E + 1] = reinterpret_cast<float (*)[kRowsPerWave][E + 1]>(lds + E * kRowStride32);
+  int (*s_wcnt)[E] = reinterpret_cast<int (*)[E]>(lds + E * kRowStride32 + kWaves * kRowsPerWave * (E + 1) * 4);
+  int* const s_base = reinterpret_cast<int*>(lds + E * kRowStride32 + kWaves * kRowsPerWave * (E + 1) * 4 +
+                                             kWaves * E * 4);
+  uint32_t* const s_mask = reinterpret_cast<uint32_t*>(s_base + E);   // tokens of each expert
+  const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
+  if (tid < kWaves * E) s_wcnt[tid / E][tid % E] = 0;   // published by the first barrier of router32_logits
+  if (tid < E) s_mask[tid] = 0u;
+  const int64_t t0 = static_cast<int64_t>(wave) * kRowsPerWave;
+  f32x4 acc[2];
+  router32_logits<NSEG>(p.x, p.w_router, p.n_tokens, t0, ws, acc);
+  RouterHist hist{};
+  hist.valid = p.valid;
+  int sel[2];                                     // experts of this lane's two slots, -1: not dispatched
+  router_tail<MEP_DTYPE_BF16, E, KC>(acc, lg[wave], nullptr, nullptr, nullptr, nullptr, nullptr, t0, p.n_tokens, KC,
+                                      p.topk_idx, p.gate, p.logits, hist, sel);
+  // rank of each entry among the wave's entries of its expert (lane order =
+  // token order; a lane's two slots hold different experts)
+  uint64_t bits0[5], bits1[5];
+#pragma unroll
+  for (int i = 0; i < 5; ++i) {
+    bits0[i] = __ballot((sel[0] >> i) & 1);
+    bits1[i] = __ballot((sel[1] >> i) & 1);
+  }
+  const uint64_t has0 = __ballot(sel[0] >= 0), has1 = __ballot(sel[1] >= 0);
+  const uint64_t before = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  int rank[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int e = sel[h];
+    const uint64_t m = e >= 0 ? (lanes_with(e, bits0, has0) | lanes_with(e, bits1, has1)) : 0ull;
+    rank[h] = __popcll(m & before);
+    if (e >= 0 && rank[h] == 0) s_wcnt[wave][e] = __popcll(m);
+    if (e >= 0) atomicOr(s_mask + e, 1u << static_cast<int>(t0 + (lane >> 2)));   // token < 32
+  }
+  __syncthreads();
+  if (tid < E) {
+    int tot = 0;
+#pragma unroll
+    for (int ww = 0; ww < kWaves; ++ww) tot += s_wcnt[ww][tid];
+    int incl = tot;                                // inclusive prefix over experts (lanes 0..31 of wave 0)
+#pragma unroll
+    for (int d = 1; d < E; d <<= 1) {
+      const int v = __shfl_up(incl, d, 64);
+      if (lane >= d) incl += v;
+    }
+    const int off = incl - tot;
+    s_base[tid] = off;
+    p.counts[tid] = tot;
+    p.offsets[tid] = off;
+    if (tid == E - 1) p.offsets[E] = incl;
+    if (p.route_counts != nullptr) p.route_counts[tid] += tot;
+  }
+  __syncthreads();
+  const int t = lane >> 2, g = lane & 3;
+  if (t0 + t < p.n_tokens) {
+    const int64_t f = (t0 + t) * KC + g * 2;
+    int row[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int e = sel[h];
+      row[h] = -1;
+      if (e >= 0) {
+        int r = s_base[e] + rank[h];
+#pragma unroll
+        for (int ww = 0; ww < kWaves; ++ww) r += ww < wave ? s_wcnt[ww][e] : 0;
+        row[h] = r;
+        p.perm[r] = static_cast<int32_t>(f + h);
+      }
+    }
+    p.row_of_entry[f] = row[0];
+    p.row_of_entry[f + 1] = row[1];
+  }
+  if (tid == 0) {
+    p.ws_flags[0] = 0u;
+    p.ws_flags[1] = 0u;
+    p.ws_header[0] = 1u;
+  }
+  // every wave's stores are in this XCD's L2; write them back to memory,
+  // then publish the records (device scope: written through to memory)
+  __syncthreads();
+  if (wave == 0) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    if (lane < E) {
+      const uint64_t rec = dec::kRecValid | (static_cast<uint64_t>(s_base[lane]) << 32) | s_mask[lane];
+      __hip_atomic_store(p.rec + lane, rec, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+// The last GEMM-2 workgroup of column block cb: out[t, cb*128 .. +128) for
+// every token, combine8's slot-order sum with device-scope reads of y, the
+// gates and row_of_entry; NaN everywhere if a routing wait gave up.  It then
+// counts the column block combined; the last column block returns the
+// poison and its own counter to zero.
+__device__ void decode_combine(const DecodeParams& p, int cb, int n_cb2, int* s_msg) {
+  const int tid = threadIdx.x;
+  const uint16_t* const y = static_cast<const uint16_t*>(p.g2.C);
+  const int H = p.g2.N;
+  const uint32_t y_bytes = static_cast<uint32_t>(p.n_tokens * 8 * H * 2);
+  if (tid == 0) s_msg[2] = atomic_read(p.sched + dec::kPoison);
+  __syncthreads();
+  const bool poison = __builtin_amdgcn_readfirstlane(s_msg[2]) != 0;
+  for (int q = tid; q < p.n_tokens * 16; q += skinny::NT) {
+    const int64_t t = q >> 4;
+    const int c = cb * 16 + (q & 15);
+    if (poison) {
+      const uint32_t nan2 = pack_bf16x2(__builtin_nanf(""), __builtin_nanf(""));
+      *reinterpret_cast<u32x4*>(p.out + t * H + c * 8) = u32x4{nan2, nan2, nan2, nan2};
+    } else {
+      auto ld = [&](const uint16_t* ptr) { return load_dev_16(y, y_bytes, static_cast<uint32_t>((ptr - y) * 2)); };
+      combine8_chunk<MEP_DTYPE_BF16, decltype(ld), true>(y, p.gate, p.row_of_entry, p.valid, t, c, H, p.out, ld);
+    }
+  }
+  if (tid == 0 && atomic_add_1(p.sched + dec::kCombined, 1) == n_cb2 - 1) {
+    atomic_add_1(p.sched + dec::kCombined, -n_cb2);
+    atomicExch(p.sched + dec::kPoison, 0);
+  }
+}
+
+// The end of workgroup 0 and of each GEMM-1 workgroup (thread 0, after its
+// stores and counts): the last of them clears the routing records for the
+// next launch (no one reads them after; GEMM-2 reads the routing itself).
+__device__ __forceinline__ void decode_exit(const DecodeParams& p) {
+  if (atomic_add_1(p.sched + dec::kSeen, 1) == p.n_g1) {
+    for (int e = 0; e < dec::E; ++e) __hip_atomic_store(p.rec + e, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    atomic_add_1(p.sched + dec::kSeen, -(p.n_g1 + 1));
+  }
+}
+
+// GEMM workgroup u of the decode launch: expert e, column block cb (see above).
+template <bool GEMM1>
+__device__ void decode_gemm(const DecodeParams& p, int u, unsigned char* lds, int* s_msg) {
+  using namespace skinny;
+  typedef uint16_t T;
+  const GemmParams& g = GEMM1 ? p.g1 : p.g2;
+  int* const sched = p.sched;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n_cb = GEMM1 ? g.N / 64 : g.N / 128;
+  const int n_cb1 = p.g1.N / 64, n_cb2 = p.g2.N / 128;
+  const int e = __builtin_amdgcn_readfirstlane(((u >> 3) / n_cb) * 8 + (u & 7));
+  const int cb = __builtin_amdgcn_readfirstlane((u >> 3) % n_cb);
+  const int n = static_cast<int>(p.n_tokens);
+  const int max_entries = n * 8;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int K = g.K, KT = K / 32, KD = K / 64;
+  const int nt = cb / 2;
+  const int rot = (!GEMM1 && KD % 4 == 0) ? 2 * (nt & 3) * (KD / 4) : 0;
+  const T* W = static_cast<const T*>(g.W) + static_cast<int64_t>(e) * g.w_expert_stride;
+  int wrow[2];
+  if constexpr (GEMM1) {
+    const int g0 = cb * 64 + wave * 16;
+    wrow[0] = g0 + lr;
+    wrow[1] = g.N + g0 + lr;
+  } else {
+    const int c0 = cb * 128 + wave * 32;
+    wrow[0] = c0 + lr;
+    wrow[1] = c0 + 16 + lr;
+  }
+  const T* wp0 = W + static_cast<int64_t>(wrow[0]) * K + 8 * lg;
+  const T* wp1 = W + static_cast<int64_t>(wrow[1]) * K + 8 * lg;
+  int* const done1 = sched + dec::kExpert + 2 * e;
+  int* const seen2 = done1 + 1;
+  u32x4 wq[DEPTH][2], aq[DEPTH][MFC];
+  auto k_off = [&](int tt) {
+    int ks = tt + rot;
+    if (ks >= KT) ks -= KT;
+    return static_cast<int64_t>(ks) * 32;
+  };
+  const int n_lds = min(LSTEPS, KT - DEPTH);
+  unsigned char* const w_lds = lds + wave * (LSTEPS * 2 * 1024);
+  auto load_w = [&](int tt, int slot) {
+    const int64_t off = k_off(tt);
+    wq[slot][0] = *reinterpret_cast<const u32x4*>(wp0 + off);
+    wq[slot][1] = *reinterpret_cast<const u32x4*>(wp1 + off);
+  };
+  auto load_w_lds = [&](int tt, int slot) {               // a step staged in LDS: [DEPTH, DEPTH + n_lds)
+    const unsigned char* b = w_lds + (tt - DEPTH) * 2048 + 16 * lane;
+    wq[slot][0] = *reinterpret_cast<const u32x4*>(b);
+    wq[slot][1] = *reinterpret_cast<const u32x4*>(b + 1024);
+  };
+  // the first DEPTH K-steps of this wave's weights to registers (each lane
+  // fetches the 16 bytes it later feeds the MFMA); GEMM-2 also stages the
+  // next n_lds steps in LDS, since it waits before its K loop.  The weights
+  // need only the expert, so this runs before any wait.
+#pragma unroll
+  for (int d = 0; d < DEPTH; ++d) load_w(d, d);
+  if constexpr (!GEMM1) {
+    const unsigned char* wb = reinterpret_cast<const unsigned char*>(W);
+    const int wbytes = static_cast<int>(g.w_expert_stride * 2);
+    const uint32_t lo0 = static_cast<uint32_t>((wp0 - W) * 2), lo1 = static_cast<uint32_t>((wp1 - W) * 2);
+    for (int tt = DEPTH; tt < DEPTH + n_lds; ++tt) {
+      const uint32_t ko = static_cast<uint32_t>(k_off(tt) * 2);
+      buffer_lds_16(wb, wbytes, lo0 + ko, 0, w_lds + (tt - DEPTH) * 2048);
+      buffer_lds_16(wb, wbytes, lo1 + ko, 0, w_lds + (tt - DEPTH) * 2048 + 1024);
+    }
+  }
+  const T* A = static_cast<const T*>(g.A);
+  const T* ap[MFC];
+  int r0 = 0, row_hi = 0, n_active = 0;
+  int cell[MFC];
+  if constexpr (!GEMM1) {
+    if (tid == 0) {
+      s_msg[3] = 0;
+      // until every GEMM-1 workgroup of the expert has stored its act rows
+      // (each adds 2 after it has seen the routing, so the rows read below
+      // are the routing's); bounded: a give-up flags and NaNs this
+      // workgroup's rows
+      const int target = 2 * n_cb1 + (e == g.dbg_chunk ? 1 : 0);
+      int polls = 0;
+      while (load_dev_i32(done1) < target) {
+        if (++polls == p.wait_limit) {
+          atomic_or_1(sched + sched::kFlags, sched::kFlagWait);
+          s_msg[3] = 1;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+      }
+      // the last GEMM-2 workgroup of the expert past the wait takes the
+      // counts back out (so a count that arrives after a give-up still
+      // leaves both at zero)
+      if (atomic_add_1(seen2, 1) == n_cb - 1) {
+        atomic_add_1(done1, -2 * n_cb1);
+        atomic_add_1(seen2, -n_cb);
+      }
+    }
+    __syncthreads();
+    // this expert's rows (at most 32), checked so that whatever a workgroup
+    // reads after a give-up stays in bounds
+    int lo = load_dev_i32(p.offsets + e), hi = load_dev_i32(p.offsets + e + 1);
+    if (lo < 0 || hi < lo || hi - lo > 16 * MFC || hi > max_entries) hi = lo = 0;
+    lo = __builtin_amdgcn_readfirstlane(lo);
+    hi = __builtin_amdgcn_readfirstlane(hi);
+    // experts with rows: one GEMM-2 workgroup each per column block
+    const int o0 = lane < dec::E ? load_dev_i32(p.offsets + lane) : 0;
+    const int o1 = lane < dec::E ? load_dev_i32(p.offsets + lane + 1) : 0;
+    n_active = __builtin_amdgcn_readfirstlane(static_cast<int>(__popcll(__ballot(lane < dec::E && o1 > o0))));
+    if (hi == lo) {
+      // no rows: nothing to compute (every token masked: expert 0's GEMM-2
+      // workgroups write the zero outputs)
+      __builtin_amdgcn_s_waitcnt(kVmcnt0);        // no DMA may still be writing LDS when the waves end
+      if (n_active == 0 && e == 0) decode_combine(p, cb, n_cb2, s_msg);
+      return;
+    }
+    r0 = lo;
+    row_hi = hi;
+#pragma unroll
+    for (int f = 0; f < MFC; ++f) {
+      const int r = min(r0 + 16 * f + lr, row_hi - 1);
+      const int c = load_dev_i32(p.perm + r);
+      cell[f] = c < 0 ? 0 : (c >= max_entries ? max_entries - 1 : c);
+      ap[f] = A + static_cast<int64_t>(r) * K + 8 * lg;   // act row
+    }
+  }
+  f32x4 acc[MFC][2];
+#pragma unroll
+  for (int f = 0; f < MFC; ++f)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[f][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  uint64_t rec = 0;                                      // GEMM-1: the expert's routing record
+  auto load_rec = [&]() { return __hip_atomic_load(p.rec + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+  if constexpr (GEMM1) {
+    // x, every token of the batch (row 16 f + lr of the MFMA is token
+    // 16 f + lr; rows past the batch repeat its last token), is the same for
+    // the four waves: it goes through an LDS ring of two blocks of DEPTH
+    // steps, laid out in MFMA lane order (step s, row fragment f: lane L's
+    // 16 bytes at (s MFC + f) KiB + 16 L).  Wave w copies rows 8 w .. 8 w + 7
+    // of a block, whole 128-byte lines (8 rows per load), into registers one
+    // block ahead and writes them after the block's MFMAs.  Read by each wave
+    // from memory instead, x would be fetched four times over in half lines
+    // and take most of the requests a CU keeps in flight, which is what
+    // bounds this loop; the weights stream into registers DEPTH steps ahead.
+    // (Plain loads and LDS writes, not LDS DMA: the compiler waits for every
+    // load in flight before reading LDS that a DMA may have written.)
+    static_assert(DEPTH == 8 && MFC == 2 && NW == 4, "a block of x is 32 rows x 4 lines, 4 loads per wave");
+    static_assert(16 * MFC == dec::kMaxTokens, "one row block holds the batch");
+    constexpr int kSlot = DEPTH * MFC * 1024;
+    unsigned char* const a_lds = lds;                    // [2][DEPTH][MFC][1 KiB]
+    const int xrow = 8 * wave + (lane >> 3), xc = lane & 7;   // row of the block, 16-byte chunk of a line
+    const unsigned char* const xsrc =
+        reinterpret_cast<const unsigned char*>(A) + static_cast<int64_t>(min(xrow, n - 1)) * K * 2 + 16 * xc;
+    // LDS offset of this lane's chunk of line i (steps 2 i, 2 i + 1)
+    const int xdst = ((xc >> 2) * MFC + (xrow >> 4)) * 1024 + ((xrow & 15) + 16 * (xc & 3)) * 16;
+    u32x4 xr[4];
+    auto load_x = [&](int b) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) xr[i] = *reinterpret_cast<const u32x4*>(xsrc + b * (DEPTH * 64) + i * 128);
+    };
+    auto write_x = [&](int b) {
+      unsigned char* const dst = a_lds + (b & 1) * kSlot + xdst;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(dst + i * (2 * MFC * 1024)) = xr[i];
+    };
+    auto block = [&](int b, bool next) {
+      const unsigned char* const src = a_lds + (b & 1) * kSlot + 16 * lane;
+#pragma unroll
+      for (int d = 0; d < DEPTH; ++d) {
+        u32x4 a[MFC];
+#pragma unroll
+        for (int f = 0; f < MFC; ++f) a[f] = *reinterpret_cast<const u32x4*>(src + (d * MFC + f) * 1024);
+#pragma unroll
+        for (int f = 0; f < MFC; ++f)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) mfma_acc(acc[f][j], wq[d][j], a[f]);
+        if (next) load_w((b + 1) * DEPTH + d, d);
+      }
+    };
+    // block b + 1 of x is loaded during block b and written after it; its
+    // slot last held block b - 1, which every wave finished before the
+    // barrier that ended block b - 1
+    const int NB = KT / DEPTH;                           // at least 4 (K = hidden >= 1024)
+    load_x(0);
+    write_x(0);
+    lds_barrier();
+    for (int b = 0; b < NB - 1; ++b) {
+      load_x(b + 1);
+      block(b, true);
+      write_x(b + 1);
+      lds_barrier();
+    }
+    // the expert's routing record, read before the last block (the routing
+    // is done by then; it is checked after the block)
+    rec = load_rec();
+    block(NB - 1, false);
+  } else {
+    // this wave's LDS steps have landed (its own lanes read them back)
+    __builtin_amdgcn_s_waitcnt(kVmcnt0);
+    __syncthreads();
+    auto load_a = [&](int tt, int slot) {
+      const int64_t off = k_off(tt);
+#pragma unroll
+      for (int f = 0; f < MFC; ++f) aq[slot][f] = *reinterpret_cast<const u32x4*>(ap[f] + off);
+    };
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) load_a(d, d);
+    k_pipeline(
+        KT,
+        [&](int d) {
+#pragma unroll
+          for (int f = 0; f < MFC; ++f)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) mfma_acc(acc[f][j], wq[d][j], aq[d][f]);
+        },
+        [&](int tt, int slot) {
+          load_w_lds(tt, slot);
+          load_a(tt, slot);
+        },
+        [&](int tt, int slot) {
+          load_w(tt, slot);
+          load_a(tt, slot);
+        },
+        [](int) {});
+  }
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+#pragma unroll
+  for (int f = 0; f < MFC; ++f)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) pin_acc(acc[f][j]);
+  T* const C = static_cast<T*>(g.C);
+  if constexpr (GEMM1) {
+    // the record read before the last block, else until it is written
+    // (bounded, each wave on its own; a give-up flags and poisons the launch,
+    // and the wave stores nothing)
+    if ((rec & dec::kRecValid) == 0 || u == p.dbg_routed) {
+      int polls = 0;
+      while ((rec & dec::kRecValid) == 0 || u == p.dbg_routed) {
+        if (++polls == p.route_wait_limit) {
+          if (lane == 0) {
+            atomic_or_1(sched + sched::kFlags, sched::kFlagWait);
+            atomic_or_1(sched + dec::kPoison, 1);
+          }
+          rec = 0;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+        rec = load_rec();
+      }
+    }
+    // token t's act row: the expert's first row plus the routed tokens
+    // before t (checked, so that a record read after a give-up stays in bounds)
+    uint32_t mask = static_cast<uint32_t>(rec) & (n >= 32 ? ~0u : (1u << n) - 1u);
+    const int first = static_cast<int>((rec >> 32) & 0xFFFFu);
+    if (first + __popc(mask) > max_entries) mask = 0u;
+#pragma unroll
+    for (int f = 0; f < MFC; ++f) {
+      const int t = 16 * f + lr;
+      if (((mask >> t) & 1u) == 0u) continue;
+      const int r = first + __popc(mask & ((1u << t) - 1u));
+      const int col = cb * 64 + wave * 16 + 4 * lg;
+      uint32_t w[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        w[h] = pack_bf16x2(silu_f(acc[f][0][2 * h]) * acc[f][1][2 * h],
+                           silu_f(acc[f][0][2 * h + 1]) * acc[f][1][2 * h + 1]);
+      uint64_t* const dst = reinterpret_cast<uint64_t*>(C + static_cast<int64_t>(r) * g.N + col);
+      __hip_atomic_store(dst, (static_cast<uint64_t>(w[1]) << 32) | w[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  } else {
+    // a GEMM-2 wait for act that gave up: NaN rows
+    if (__builtin_amdgcn_readfirstlane(s_msg[3])) {
+      const float nan = __builtin_nanf("");
+#pragma unroll
+      for (int f = 0; f < MFC; ++f)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[f][j] = f32x4{nan, nan, nan, nan};
+    }
+#pragma unroll
+    for (int f = 0; f < MFC; ++f) {
+      const int r = r0 + 16 * f + lr;
+      if (r >= row_hi) continue;
+      const int64_t row = cell[f];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int col = cb * 128 + wave * 32 + 16 * j + 4 * lg;
+        const uint2 w = make_uint2(pack_bf16x2(acc[f][j][0], acc[f][j][1]), pack_bf16x2(acc[f][j][2], acc[f][j][3]));
+        __hip_atomic_store(reinterpret_cast<uint64_t*>(C + row * g.N + col), (static_cast<uint64_t>(w.y) << 32) | w.x,
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+  // every wave's stores are complete before the counts go up
+  __builtin_amdgcn_s_waitcnt(kVmcnt0);
+  __syncthreads();
+  if constexpr (GEMM1) {
+    if (tid == 0) {
+      atomic_add_1(done1, 2);
+      decode_exit(p);
+    }
+  } else {
+    // the last GEMM-2 workgroup of the column block combines it
+    if (tid == 0) {
+      const int c = atomic_add_1(sched + dec::kCol + cb, 1);
+      s_msg[1] = c == n_active - 1;
+      if (c == n_active - 1) atomic_add_1(sched + dec::kCol + cb, -n_active);
+    }
+    __syncthreads();
+    if (__builtin_amdgcn_readfirstlane(s_msg[1])) decode_combine(p, cb, n_cb2, s_msg);
+  }
+}
+
+template <int NSEG>
+__global__ __launch_bounds__(skinny::NT) void moe_decode_kernel(DecodeParams p) {
+  __shared__ __attribute__((aligned(16))) unsigned char lds[dec::kLds];
+  __shared__ int s_msg[4];
+  const int b = blockIdx.x;
+  if (b == 0) {
+    decode_route<NSEG>(p, lds);
+    if (threadIdx.x == 0) decode_exit(p);
+  } else if (b <= p.n_g1) {
+    decode_gemm<true>(p, b - 1, lds, s_msg);
+  } else {
+    decode_gemm<false>(p, b - 1 - p.n_g1, lds, s_msg);
+  }
 }
 
 // XCD queues of a device with n_cu compute units: one per 32 CUs (8 on a
@@ -2201,4 +2788,112 @@ extern "C" int mep_grouped_swiglu_combine(const void* x, int64_t n_tokens, int32
                         fuse ? &cp : nullptr, &combined);
   if (rc != MEP_OK || combined) return rc;
   return mep_combine(y_entries, topk_gate, row_of_entry, valid_mask, n_tokens, top_k, hidden, dtype, out, stream);
+}
+
+namespace mep {
+namespace {
+
+// The decode layer's one launch, if it applies: bf16, 32 experts, top-8,
+// 1..32 tokens, hidden 1024 / 2048 / 4096, inter a multiple of 256, and a
+// schedule buffer of dec::words(hidden) ints; otherwise hipErrorNotSupported
+// with nothing enqueued.
+hipError_t launch_decode(const void* x, const void* w_router, const uint8_t* valid, int64_t n_tokens, int hidden,
+                         int E, int k, int dtype, const void* w_in, const void* w_out, int inter, int64_t* topk_idx,
+                         void* gate, float* logits, int32_t* counts, int32_t* offsets, int32_t* perm,
+                         int32_t* row_of_entry, int64_t* route_counts, void* y_entries, void* dispatch_ws,
+                         void* act, int32_t* tile_queue, size_t tile_queue_ints, void* out, hipStream_t stream) {
+  if (dtype != MEP_DTYPE_BF16 || E != dec::E || k != 8 || n_tokens < 1 || n_tokens > dec::kMaxTokens ||
+      inter % 256 != 0 || static_cast<int64_t>(tile_queue_ints) < dec::words(hidden))
+    return hipErrorNotSupported;
+  if (hidden != 1024 && hidden != 2048 && hidden != 4096) return hipErrorNotSupported;
+  DecodeParams p{};
+  p.x = static_cast<const uint16_t*>(x);
+  p.w_router = static_cast<const uint16_t*>(w_router);
+  p.valid = valid;
+  p.n_tokens = n_tokens;
+  p.topk_idx = topk_idx;
+  p.gate = static_cast<uint16_t*>(gate);
+  p.logits = logits;
+  p.counts = counts;
+  p.offsets = offsets;
+  p.perm = perm;
+  p.row_of_entry = row_of_entry;
+  p.route_counts = route_counts;
+  p.ws_header = static_cast<uint32_t*>(dispatch_ws);
+  p.ws_flags = reinterpret_cast<uint32_t*>(static_cast<char*>(dispatch_ws) + kWsHeaderBytes);
+  const int64_t max_rows = n_tokens * k;
+  p.g1 = gemm1_params<MEP_DTYPE_BF16, CfgBf16>(x, n_tokens, k, perm, offsets, E, w_in, nullptr, hidden, inter, act);
+  p.g2 = gemm2_params<MEP_DTYPE_BF16, CfgBf16>(act, k, perm, offsets, E, max_rows, w_out, nullptr, hidden, inter,
+                                               y_entries);
+  set_sched(p.g1, tile_queue);
+  set_sched(p.g2, tile_queue);
+  p.out = static_cast<uint16_t*>(out);
+  p.n_g1 = E * (inter / 64);
+  p.n_g2 = E * (hidden / 128);
+  p.sched = tile_queue;
+  const GiveupTest gt = giveup_test();
+  p.wait_limit = gt.site == MEP_GIVEUP_CHUNK ? gt.polls : sched::kWaitLimit;
+  p.route_wait_limit = gt.site == MEP_GIVEUP_ROUTED ? gt.polls : sched::kWaitLimit;
+  p.dbg_routed = gt.site == MEP_GIVEUP_ROUTED ? 0 : -1;
+  p.rec = reinterpret_cast<uint64_t*>(tile_queue + dec::kRec(hidden));
+  const dim3 grid(static_cast<unsigned>(1 + p.n_g1 + p.n_g2));
+  switch (hidden) {
+    case 1024: moe_decode_kernel<1><<<grid, skinny::NT, 0, stream>>>(p); break;
+    case 2048: moe_decode_kernel<2><<<grid, skinny::NT, 0, stream>>>(p); break;
+    default: moe_decode_kernel<4><<<grid, skinny::NT, 0, stream>>>(p); break;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+}  // namespace mep
+
+extern "C" size_t mep_moe_layer_queue_ints(int64_t n_tokens, int32_t n_experts, int32_t hidden) {
+  if (n_tokens < 0 || n_experts <= 0 || hidden <= 0) return 0;
+  const int64_t a = mep::sched::words(n_tokens * 8, n_experts), b = mep::dec::words(hidden);
+  return static_cast<size_t>(a > b ? a : b);
+}
+
+extern "C" int mep_moe_layer(const void* x, const void* w_router, const uint8_t* valid_mask, int64_t n_tokens,
+                             int32_t hidden, int32_t n_experts, int32_t top_k, int32_t dtype, const void* w_in,
+                             const void* w_out, int32_t inter, int64_t* topk_idx, void* topk_gate, float* logits,
+                             int32_t* counts, int32_t* offsets, int32_t* perm, int32_t* row_of_entry,
+                             int64_t* route_counts, void* y_entries, void* dispatch_ws, size_t dispatch_ws_bytes,
+                             void* experts_ws, size_t experts_ws_bytes, int32_t* tile_queue, size_t tile_queue_ints,
+                             void* out, void* stream) {
+  clear_error();
+  const char* fn = "mep_moe_layer";
+  MEP_REQUIRE(n_tokens >= 0, MEP_ERR_INVALID_ARG, "%s: n_tokens < 0", fn);
+  MEP_REQUIRE(dispatch_ws != nullptr && experts_ws != nullptr && tile_queue != nullptr, MEP_ERR_INVALID_ARG,
+              "%s: null workspace or tile_queue", fn);
+  MEP_REQUIRE(dispatch_ws_bytes >= mep_route_dispatch_workspace_size(n_tokens, n_experts), MEP_ERR_WORKSPACE,
+              "%s: dispatch workspace %zu B < required %zu B", fn, dispatch_ws_bytes,
+              mep_route_dispatch_workspace_size(n_tokens, n_experts));
+  const int64_t max_rows = n_tokens * top_k;
+  MEP_REQUIRE(experts_ws_bytes >= mep_experts_workspace_size(max_rows, inter, dtype), MEP_ERR_WORKSPACE,
+              "%s: experts workspace %zu B < required %zu B", fn, experts_ws_bytes,
+              mep_experts_workspace_size(max_rows, inter, dtype));
+  if (n_tokens > 0) {
+    MEP_REQUIRE(x && w_router && w_in && w_out && topk_idx && topk_gate && counts && offsets && perm &&
+                    row_of_entry && y_entries && out,
+                MEP_ERR_INVALID_ARG, "%s: null pointer", fn);
+    MEP_REQUIRE(aligned16(x) && aligned16(w_in) && aligned16(w_out) && aligned16(experts_ws) &&
+                    aligned16(y_entries) && aligned16(out) && aligned16(topk_gate),
+                MEP_ERR_INVALID_ARG, "%s: buffers must be 16-byte aligned", fn);
+    const hipError_t e = launch_decode(x, w_router, valid_mask, n_tokens, hidden, n_experts, top_k, dtype, w_in, w_out,
+                                       inter, topk_idx, topk_gate, logits, counts, offsets, perm, row_of_entry,
+                                       route_counts, y_entries, dispatch_ws, experts_ws, tile_queue, tile_queue_ints,
+                                       out, static_cast<hipStream_t>(stream));
+    if (e == hipSuccess) return MEP_OK;
+    MEP_REQUIRE(e == hipErrorNotSupported, MEP_ERR_HIP, "%s: launch failed: %s", fn, hipGetErrorString(e));
+  }
+  // the two calls: router + dispatch, then the experts ending with the combine
+  int rc = mep_route_dispatch(x, w_router, valid_mask, n_tokens, hidden, n_experts, top_k, dtype, topk_idx, topk_gate,
+                              logits, counts, offsets, perm, row_of_entry, route_counts, dispatch_ws,
+                              dispatch_ws_bytes, stream);
+  if (rc != MEP_OK) return rc;
+  if (n_tokens == 0) return MEP_OK;
+  return mep_grouped_swiglu_combine(x, n_tokens, top_k, perm, offsets, row_of_entry, topk_gate, valid_mask, n_experts,
+                                    max_rows, w_in, w_out, hidden, inter, dtype, y_entries, experts_ws,
+                                    experts_ws_bytes, tile_queue, tile_queue_ints, out, stream);
 }

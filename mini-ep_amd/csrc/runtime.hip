@@ -47,7 +47,7 @@ GiveupTest giveup_test() {
 
 extern "C" int mep_test_force_giveup(int32_t site, int32_t polls) {
   mep::clear_error();
-  MEP_REQUIRE(site >= MEP_GIVEUP_NONE && site <= MEP_GIVEUP_COMBINE, MEP_ERR_INVALID_ARG,
+  MEP_REQUIRE(site >= MEP_GIVEUP_NONE && site <= MEP_GIVEUP_ROUTED, MEP_ERR_INVALID_ARG,
               "mep_test_force_giveup: unknown site %d", site);
   MEP_REQUIRE(site == MEP_GIVEUP_NONE || polls > 0, MEP_ERR_INVALID_ARG,
               "mep_test_force_giveup: polls must be positive (got %d)", polls);

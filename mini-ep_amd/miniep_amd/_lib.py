@@ -34,6 +34,7 @@ GIVEUP_DISPATCH = 1
 GIVEUP_ROWS = 2
 GIVEUP_CHUNK = 3
 GIVEUP_COMBINE = 4
+GIVEUP_ROUTED = 5
 
 
 class MepError(RuntimeError):
@@ -109,6 +110,11 @@ _SIGNATURES = {
     "mep_combine_rows": (ctypes.c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i32,
                                         _i32, _i32, _c_void_p, _c_void_p]),
     "mep_test_force_giveup": (ctypes.c_int, [_i32, _i32]),
+    "mep_moe_layer_queue_ints": (_size, [_i64, _i32, _i32]),
+    "mep_moe_layer": (ctypes.c_int, [_c_void_p, _c_void_p, _c_void_p, _i64, _i32, _i32, _i32, _i32, _c_void_p,
+                                     _c_void_p, _i32, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                     _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _size, _c_void_p, _size,
+                                     _c_void_p, _size, _c_void_p, _c_void_p]),
 }
 
 _LIB = None

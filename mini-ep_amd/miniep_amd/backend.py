@@ -68,14 +68,15 @@ class HipMoEBackend:
 
     def route_and_call(self, x_flat, w_router, k, valid_mask=None):
         """The router hook and this backend in one go (Block.forward,
-        modeling.py:193-196): the router kernel also builds the dispatch
-        histograms (ops.route_dispatch), one launch fewer than route() +
-        __call__, same results.  Returns (out, topk_idx, topk_gate)."""
+        modeling.py:193-196) through ops.moe_layer: the router kernel also
+        builds the dispatch, and decode batches run router, experts and
+        combine as one launch; same results as route() + __call__.  Returns
+        (out, topk_idx, topk_gate)."""
         x = x_flat.to(self.w_in.dtype)
-        idx, gate, disp = ops.route_dispatch(x, w_router, k, valid_mask, check=self.check)
+        out, idx, gate, disp = ops.moe_layer(x, w_router, k, self.w_in, self.w_out, valid_mask)
         self.last_dispatch = disp
-        out = ops.grouped_swiglu_combine(x, disp, self.w_in, self.w_out, gate, valid_mask)
         if self.check:
+            ops.dispatch_check(out.device)
             ops.experts_check(out.device)
         return out, idx, gate
 

@@ -78,6 +78,16 @@ def _dispatch_workspace(dev: torch.device, nbytes: int) -> torch.Tensor:
     return ws
 
 
+def dispatch_check(dev: torch.device | None = None) -> None:
+    """Synchronise and raise MepError if the last dispatch on the current
+    stream of ``dev`` (its workspace) dropped entries or gave up waiting."""
+    dev = dev or torch.device("cuda", torch.cuda.current_device())
+    key = (dev.index if dev.index is not None else torch.cuda.current_device(), _stream(dev))
+    ws = _DISPATCH_WS.get(key)
+    if ws is not None:
+        _lib.check(_lib.lib().mep_dispatch_check(ws.data_ptr(), _stream(dev)), "mep_dispatch_check")
+
+
 def experts_check(dev: torch.device | None = None) -> None:
     """Synchronise and raise MepError if a grouped-GEMM launch on the current
     stream of ``dev`` flagged its results invalid (a GEMM-2 tile that gave
@@ -341,6 +351,62 @@ def grouped_swiglu_combine(x_flat: torch.Tensor, disp: Dispatch, w_in: torch.Ten
                                       out.data_ptr(), _stream(dev))
     _lib.check(rc, "mep_grouped_swiglu_combine")
     return out
+
+
+def moe_layer(x_flat: torch.Tensor, w_router: torch.Tensor, k: int, w_in: torch.Tensor, w_out: torch.Tensor,
+              valid_mask: torch.Tensor | None = None, route_counts: torch.Tensor | None = None,
+              return_logits: bool = False):
+    """The MoE block of the all-local backend in one call (mep_moe_layer):
+    route_dispatch followed by grouped_swiglu_combine, the same bits;
+    returns (out, topk_idx, topk_gate, Dispatch[, logits]).  Decode batches of
+    GraniteMoE's shape (bf16, 32 experts, top-8, at most 32 tokens) run as one
+    launch."""
+    dev = _require_device(x_flat, w_router, w_in, w_out, valid_mask, route_counts)
+    x = x_flat.contiguous()
+    n, h = x.shape
+    w = w_router.to(x.dtype).contiguous()
+    e = w.shape[0]
+    if w.shape[1] != h or w_in.dim() != 3 or w_out.dim() != 3:
+        raise ValueError("w_router must be (E, H), w_in (E, 2I, H) and w_out (E, H, I)")
+    e_loc, two_i, h_in = w_in.shape
+    inter = two_i // 2
+    if e_loc != e or h_in != h or tuple(w_out.shape) != (e, h, inter):
+        raise ValueError(f"weight shapes {tuple(w_in.shape)} / {tuple(w_out.shape)} do not match "
+                         f"hidden {h} and {e} experts")
+    if route_counts is not None and (route_counts.dtype != torch.int64 or route_counts.numel() != e):
+        raise TypeError("route_counts must be an int64 tensor of n_experts")
+    wi = w_in.to(x.dtype).contiguous()
+    wo = w_out.to(x.dtype).contiguous()
+    vm = _mask_u8(valid_mask, n)
+    L = _lib.lib()
+    code = _dtype_code(x)
+    idx = torch.empty((n, k), dtype=torch.int64, device=dev)
+    gate = torch.empty((n, k), dtype=x.dtype, device=dev)
+    logits = torch.empty((n, e), dtype=torch.float32, device=dev) if return_logits else None
+    nk = max(n * k, 1)
+    counts = torch.empty(e, dtype=torch.int32, device=dev)
+    offsets = torch.empty(e + 1, dtype=torch.int32, device=dev)
+    perm = torch.empty(nk, dtype=torch.int32, device=dev)
+    row_of_entry = torch.empty(nk, dtype=torch.int32, device=dev)
+    y = torch.empty((nk, h), dtype=x.dtype, device=dev)
+    out = torch.empty((n, h), dtype=x.dtype, device=dev)
+    dws = _dispatch_workspace(dev, int(L.mep_route_dispatch_workspace_size(n, e)))
+    max_rows = n * k
+    ews = torch.empty(max(int(L.mep_experts_workspace_size(max_rows, inter, code)), 256), dtype=torch.uint8,
+                      device=dev)
+    need = int(L.mep_moe_layer_queue_ints(n, e, h))
+    key = (dev.index if dev.index is not None else torch.cuda.current_device(), _stream(dev))
+    tq = _QUEUES.get(key)
+    if tq is None or tq.numel() < need:
+        tq = _QUEUES[key] = torch.zeros(max(need, 64), dtype=torch.int32, device=dev)
+    rc = L.mep_moe_layer(x.data_ptr(), w.data_ptr(), _ptr(vm), n, h, e, k, code, wi.data_ptr(), wo.data_ptr(), inter,
+                         idx.data_ptr(), gate.data_ptr(), _ptr(logits), counts.data_ptr(), offsets.data_ptr(),
+                         perm.data_ptr(), row_of_entry.data_ptr(), _ptr(route_counts), y.data_ptr(), dws.data_ptr(),
+                         dws.numel(), ews.data_ptr(), ews.numel(), tq.data_ptr(), tq.numel(), out.data_ptr(),
+                         _stream(dev))
+    _lib.check(rc, "mep_moe_layer")
+    d = Dispatch(counts, offsets, perm, row_of_entry, None, n, k, e)
+    return (out, idx, gate, d) + ((logits,) if return_logits else ())
 
 
 def copy_experts(src_in: torch.Tensor, src_out: torch.Tensor, src_index: list[int], dst_in: torch.Tensor,

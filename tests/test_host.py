@@ -19,7 +19,7 @@ from oracle import moe_oracle as O
 def test_library_exports_every_header_function():
     L = _lib.lib()
     names = _lib.header_functions()
-    assert len(names) == 23
+    assert len(names) == 25
     for n in names:
         assert hasattr(L, n), n
     assert L.mep_abi_version() == 5
