@@ -162,18 +162,19 @@ def mfma_busy_from_profile() -> dict | None:
     return None
 
 
-def decode_detail(dev, calls: int = 200) -> dict:
+def decode_detail(dev, calls: int = 200, graph_calls: int = 24) -> dict:
     """The decode-shaped layer (32 tokens, bf16, unbiased router: near-uniform
     load, most experts with 0-16 entries), HBM-bound on streaming the expert
-    weights of the experts it touches.  One call = route + dispatch (one
-    launch), then GEMM-1, GEMM-2 and the combine (one launch)
-    (HipMoEBackend.route_and_call, 2 launches).  At this size
-    the host's enqueue time is close to the GPU time, so the call is also
-    captured in a HIP graph and replayed (a decode loop could replay it the
-    same way); every replay is checked against the eager output.  HIP events
-    around `calls` back-to-back calls, eager and replayed.  Roofline: the
-    touched experts' weight bytes (3 H I bf16 each) + x, y and outputs per
-    call over the faster call time, vs the 8 TB/s HBM peak."""
+    weights of the experts it touches.  One call = HipMoEBackend.route_and_call:
+    router, dispatch, GEMM-1, GEMM-2 and the combine in one launch
+    (mep_moe_layer).  At this size the host's enqueue time is close to the GPU
+    time, so the calls are also captured in a HIP graph, `graph_calls` in a
+    row as a decode step's layers would be (one replay per step amortises the
+    graph launch), and replayed; every replayed call is checked against the
+    eager output.  HIP events around `calls` back-to-back calls, eager and
+    replayed.  Roofline: the touched experts' weight bytes (3 H I bf16 each)
+    + x, y and outputs per call over the faster call time, vs the 8 TB/s HBM
+    peak."""
     import torch
 
     from miniep_amd import HipMoEBackend, workloads
@@ -210,17 +211,17 @@ def decode_detail(dev, calls: int = 200) -> dict:
     # workspaces per stream, and a first call inside the capture would record
     # their one-time fill into every replay
     with torch.cuda.graph(graph, stream=side):
-        out = be.route_and_call(x, w_r, K)[0]
+        outs = [be.route_and_call(x, w_r, K)[0] for _ in range(graph_calls)]
     replays_equal = True
     for _ in range(3):
         graph.replay()
         torch.cuda.synchronize()
-        replays_equal &= bool(torch.equal(out, ref))
+        replays_equal &= all(bool(torch.equal(o, ref)) for o in outs)
         be.route_and_call(x, w_r, K)
         torch.cuda.synchronize()
-    ms = timed(graph.replay)
+    ms = timed(graph.replay) / graph_calls
     torch.cuda.synchronize()
-    replays_equal &= bool(torch.equal(out, ref))
+    replays_equal &= all(bool(torch.equal(o, ref)) for o in outs)
     touched = int((be.last_dispatch.counts > 0).sum())
     H, I = workloads.HIDDEN, workloads.INTER
     nbytes = touched * 3 * H * I * 2 + T * H * 2 * 2 + T * K * H * 2 * 2
@@ -229,8 +230,9 @@ def decode_detail(dev, calls: int = 200) -> dict:
             "us_per_call": 1e3 * best, "us_per_call_eager": 1e3 * eager_ms, "us_per_call_graph": 1e3 * ms,
             "replays_equal_eager": replays_equal, "bytes": nbytes, "GB/s": nbytes / (best / 1e3) / 1e9,
             "frac_hbm": nbytes / (best / 1e3) / PEAK_HBM_BYTES, "floor_us": 1e6 * nbytes / PEAK_HBM_BYTES,
-            "measures": f"route_and_call (2 launches), {calls} calls back to back, HIP events, launched from Python "
-                        "(eager) and replayed from a HIP graph (graph); us_per_call is the faster of the two"}
+            "measures": f"route_and_call (one launch), {calls} calls back to back, HIP events, launched from Python "
+                        f"(eager) and from a HIP graph of {graph_calls} calls replayed {calls} times (graph, per "
+                        "call); us_per_call is the faster of the two"}
 
 
 def blas_reference(dev, M: int) -> dict:

@@ -1870,11 +1870,12 @@ hipError_t launch_skinny_both(const GemmParams& p1, const GemmParams& p2, int64_
 // t (the block lists its entries in token order).  A row's MFMA result
 // depends only on that row, in the same K order and with the same MFMAs as
 // skinny_body, so act has the two-call path's bits.  Each GEMM-1 workgroup
-// then adds 2 to its expert's count; the last of workgroup 0 and the GEMM-1
-// workgroups to finish clears the records for the next launch.  GEMM-2
-// workgroups stream their weights (all of K = 512: registers + LDS) up
-// front, wait only for that count to reach twice the GEMM-1 column blocks,
-// then read the rows (written before the records) and act.  The combine has
+// then adds 2 to its expert's count.  GEMM-2 workgroups stream their
+// weights (all of K = 512: registers + LDS) up front, wait for their
+// expert's record and read its rows and destination cells (written before
+// the records), then wait for that count to reach twice the GEMM-1 column
+// blocks and read act.  The last user of a record clears it for the next
+// launch.  The combine has
 // no wait of its own: the last GEMM-2 workgroup of a column block to finish
 // (one per expert with rows) combines that column block for every token
 // (combine8_chunk, the same slot-order sum as mep_combine), reading y, the
@@ -1885,19 +1886,29 @@ hipError_t launch_skinny_both(const GemmParams& p1, const GemmParams& p2, int64_
 namespace dec {
 constexpr int kMaxTokens = 32;
 constexpr int E = 32;
-constexpr int kSeen = 15;                               // workgroups done with the routing records
-constexpr int kExpert = sched::kRowDone;                // [16, 16 + 2E): per expert GEMM-1 counts, GEMM-2 readers
-constexpr int kPoison = sched::kRowDone + 2 * E;        // a routing wait gave up
+// Schedule words.  Counters that many workgroups update each sit in a
+// 256-byte block of their own: device-scope atomics on one line are
+// performed one after another where that line lives, and a few hundred of
+// them on one line put microseconds of queueing in front of every count
+// behind them.
+constexpr int kPoison = sched::kRowDone;                // a routing wait gave up
 constexpr int kCombined = kPoison + 1;                  // column blocks combined
-constexpr int kCol = kCombined + 1;                     // [.., + H / 128): GEMM-2 workgroups done per column block
-// [kRec(H), + 2E): the routing record of each expert, one 64-bit word:
-// bit 63 set once written, bits 32..47 the expert's first row, bits 0..31
-// its tokens (bit t: token t is routed to the expert)
-inline int kRec(int hidden) { return (kCol + hidden / 128 + 1) & ~1; }
+constexpr int kBlock = 64;                              // ints per counter block
+// expert e's block: GEMM-1 count, GEMM-2 workgroups past their wait, users
+// done with the routing record, and the record itself (one 64-bit word: bit
+// 63 set once written, bits 32..47 the expert's first row, bits 0..31 its
+// tokens, bit t for token t)
+__host__ __device__ constexpr int kExp(int e) { return kBlock * (1 + e); }
+constexpr int kDone1 = 0, kSeen2 = 1, kUsers = 2, kRecWord = 4;
+// column block cb's block: GEMM-2 workgroups done with it
+__host__ __device__ constexpr int kColBlk(int cb) { return kBlock * (1 + E + cb); }
 constexpr uint64_t kRecValid = 1ull << 63;
 constexpr int kRouterLds = E * kRowStride32 + kWaves * kRowsPerWave * (E + 1) * 4 + kWaves * E * 4 + 2 * E * 4;
 constexpr int kLds = kRouterLds > skinny::LDS_W ? kRouterLds : skinny::LDS_W;
-inline int64_t words(int hidden) { return kRec(hidden) + 2 * E; }
+inline int64_t words(int hidden) { return kColBlk(hidden / 128); }
+__device__ __forceinline__ uint64_t* rec_word(int* sched, int e) {
+  return reinterpret_cast<uint64_t*>(sched + kExp(e) + kRecWord);
+}
 }  // namespace dec
 
 struct DecodeParams {
@@ -1922,12 +1933,23 @@ struct DecodeParams {
   int wait_limit;                // polls before GEMM-2's wait for act gives up
   int route_wait_limit;          // polls before GEMM-1's wait for its routing record gives up
   int dbg_routed;                // GEMM-1 workgroup whose routing wait cannot end (test hook; -1: none)
-  uint64_t* rec;                 // the routing records (in sched)
 };
 
 // Device-scope 32-bit load (written earlier in this launch, possibly on another XCD).
 __device__ __forceinline__ int load_dev_i32(const int32_t* q) {
   return __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// A user of expert e's routing record is done with it (workgroup 0 after
+// writing it, every GEMM-1 and GEMM-2 workgroup of the expert after reading
+// it): the last of them clears it for the next launch.
+__device__ __forceinline__ void decode_rec_done(const DecodeParams& p, int e) {
+  int* const users = p.sched + dec::kExp(e) + dec::kUsers;
+  const int n = 1 + p.g1.N / 64 + p.g2.N / 128;
+  if (atomic_add_1(users, 1) == n - 1) {
+    __hip_atomic_store(dec::rec_word(p.sched, e), 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    atomic_add_1(users, -n);
+  }
 }
 
 // Workgroup 0: route the batch (router32_logits, router_tail: the fused
@@ -2022,7 +2044,11 @@ __device__ void decode_route(const DecodeParams& p, unsigned char* lds) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
     if (lane < E) {
       const uint64_t rec = dec::kRecValid | (static_cast<uint64_t>(s_base[lane]) << 32) | s_mask[lane];
-      __hip_atomic_store(p.rec + lane, rec, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(dec::rec_word(p.sched, lane), rec, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      // workgroup 0 is one of the record's users: its count follows the
+      // record, so that whoever clears it does so after it landed
+      __builtin_amdgcn_s_waitcnt(kVmcnt0);
+      decode_rec_done(p, lane);
     }
   }
 }
@@ -2057,16 +2083,6 @@ __device__ void decode_combine(const DecodeParams& p, int cb, int n_cb2, int* s_
   }
 }
 
-// The end of workgroup 0 and of each GEMM-1 workgroup (thread 0, after its
-// stores and counts): the last of them clears the routing records for the
-// next launch (no one reads them after; GEMM-2 reads the routing itself).
-__device__ __forceinline__ void decode_exit(const DecodeParams& p) {
-  if (atomic_add_1(p.sched + dec::kSeen, 1) == p.n_g1) {
-    for (int e = 0; e < dec::E; ++e) __hip_atomic_store(p.rec + e, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    atomic_add_1(p.sched + dec::kSeen, -(p.n_g1 + 1));
-  }
-}
-
 // GEMM workgroup u of the decode launch: expert e, column block cb (see above).
 template <bool GEMM1>
 __device__ void decode_gemm(const DecodeParams& p, int u, unsigned char* lds, int* s_msg) {
@@ -2098,8 +2114,12 @@ __device__ void decode_gemm(const DecodeParams& p, int u, unsigned char* lds, in
   }
   const T* wp0 = W + static_cast<int64_t>(wrow[0]) * K + 8 * lg;
   const T* wp1 = W + static_cast<int64_t>(wrow[1]) * K + 8 * lg;
-  int* const done1 = sched + dec::kExpert + 2 * e;
-  int* const seen2 = done1 + 1;
+  int* const done1 = sched + dec::kExp(e) + dec::kDone1;
+  int* const seen2 = sched + dec::kExp(e) + dec::kSeen2;
+  uint64_t rec = 0;                                      // the expert's routing record
+  auto load_rec = [&]() {
+    return __hip_atomic_load(dec::rec_word(sched, e), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  };
   u32x4 wq[DEPTH][2], aq[DEPTH][MFC];
   auto k_off = [&](int tt) {
     int ks = tt + rot;
@@ -2141,10 +2161,46 @@ __device__ void decode_gemm(const DecodeParams& p, int u, unsigned char* lds, in
   if constexpr (!GEMM1) {
     if (tid == 0) {
       s_msg[3] = 0;
-      // until every GEMM-1 workgroup of the expert has stored its act rows
-      // (each adds 2 after it has seen the routing, so the rows read below
-      // are the routing's); bounded: a give-up flags and NaNs this
+      // the routing is complete once the expert's record is written (after
+      // workgroup 0's other stores reached memory), so the rows are read
+      // while GEMM-1 still runs; bounded: a give-up flags and NaNs this
       // workgroup's rows
+      int polls = 0;
+      while ((load_rec() & dec::kRecValid) == 0) {
+        if (++polls == p.wait_limit) {
+          atomic_or_1(sched + sched::kFlags, sched::kFlagWait);
+          s_msg[3] = 1;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+      }
+      decode_rec_done(p, e);                             // done with the record
+    }
+    __syncthreads();
+    // this expert's rows (at most 32), checked so that whatever a workgroup
+    // reads after a give-up stays in bounds
+    int lo = load_dev_i32(p.offsets + e), hi = load_dev_i32(p.offsets + e + 1);
+    if (lo < 0 || hi < lo || hi - lo > 16 * MFC || hi > max_entries) hi = lo = 0;
+    lo = __builtin_amdgcn_readfirstlane(lo);
+    hi = __builtin_amdgcn_readfirstlane(hi);
+    // experts with rows: one GEMM-2 workgroup each per column block
+    const int o0 = lane < dec::E ? load_dev_i32(p.offsets + lane) : 0;
+    const int o1 = lane < dec::E ? load_dev_i32(p.offsets + lane + 1) : 0;
+    n_active = __builtin_amdgcn_readfirstlane(static_cast<int>(__popcll(__ballot(lane < dec::E && o1 > o0))));
+    r0 = lo;
+    row_hi = hi;
+    if (hi > lo) {
+#pragma unroll
+      for (int f = 0; f < MFC; ++f) {
+        const int r = min(r0 + 16 * f + lr, row_hi - 1);
+        const int c = load_dev_i32(p.perm + r);
+        cell[f] = c < 0 ? 0 : (c >= max_entries ? max_entries - 1 : c);
+        ap[f] = A + static_cast<int64_t>(r) * K + 8 * lg;   // act row
+      }
+    }
+    if (tid == 0) {
+      // until every GEMM-1 workgroup of the expert has stored its act rows
+      // (each adds 2 after them); bounded as above
       const int target = 2 * n_cb1 + (e == g.dbg_chunk ? 1 : 0);
       int polls = 0;
       while (load_dev_i32(done1) < target) {
@@ -2164,16 +2220,6 @@ __device__ void decode_gemm(const DecodeParams& p, int u, unsigned char* lds, in
       }
     }
     __syncthreads();
-    // this expert's rows (at most 32), checked so that whatever a workgroup
-    // reads after a give-up stays in bounds
-    int lo = load_dev_i32(p.offsets + e), hi = load_dev_i32(p.offsets + e + 1);
-    if (lo < 0 || hi < lo || hi - lo > 16 * MFC || hi > max_entries) hi = lo = 0;
-    lo = __builtin_amdgcn_readfirstlane(lo);
-    hi = __builtin_amdgcn_readfirstlane(hi);
-    // experts with rows: one GEMM-2 workgroup each per column block
-    const int o0 = lane < dec::E ? load_dev_i32(p.offsets + lane) : 0;
-    const int o1 = lane < dec::E ? load_dev_i32(p.offsets + lane + 1) : 0;
-    n_active = __builtin_amdgcn_readfirstlane(static_cast<int>(__popcll(__ballot(lane < dec::E && o1 > o0))));
     if (hi == lo) {
       // no rows: nothing to compute (every token masked: expert 0's GEMM-2
       // workgroups write the zero outputs)
@@ -2181,23 +2227,12 @@ __device__ void decode_gemm(const DecodeParams& p, int u, unsigned char* lds, in
       if (n_active == 0 && e == 0) decode_combine(p, cb, n_cb2, s_msg);
       return;
     }
-    r0 = lo;
-    row_hi = hi;
-#pragma unroll
-    for (int f = 0; f < MFC; ++f) {
-      const int r = min(r0 + 16 * f + lr, row_hi - 1);
-      const int c = load_dev_i32(p.perm + r);
-      cell[f] = c < 0 ? 0 : (c >= max_entries ? max_entries - 1 : c);
-      ap[f] = A + static_cast<int64_t>(r) * K + 8 * lg;   // act row
-    }
   }
   f32x4 acc[MFC][2];
 #pragma unroll
   for (int f = 0; f < MFC; ++f)
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[f][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  uint64_t rec = 0;                                      // GEMM-1: the expert's routing record
-  auto load_rec = [&]() { return __hip_atomic_load(p.rec + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
   if constexpr (GEMM1) {
     // x, every token of the batch (row 16 f + lr of the MFMA is token
     // 16 f + lr; rows past the batch repeat its last token), is the same for
@@ -2363,14 +2398,15 @@ __device__ void decode_gemm(const DecodeParams& p, int u, unsigned char* lds, in
   if constexpr (GEMM1) {
     if (tid == 0) {
       atomic_add_1(done1, 2);
-      decode_exit(p);
+      decode_rec_done(p, e);
     }
   } else {
     // the last GEMM-2 workgroup of the column block combines it
     if (tid == 0) {
-      const int c = atomic_add_1(sched + dec::kCol + cb, 1);
+      int* const col = sched + dec::kColBlk(cb);
+      const int c = atomic_add_1(col, 1);
       s_msg[1] = c == n_active - 1;
-      if (c == n_active - 1) atomic_add_1(sched + dec::kCol + cb, -n_active);
+      if (c == n_active - 1) atomic_add_1(col, -n_active);
     }
     __syncthreads();
     if (__builtin_amdgcn_readfirstlane(s_msg[1])) decode_combine(p, cb, n_cb2, s_msg);
@@ -2384,7 +2420,6 @@ __global__ __launch_bounds__(skinny::NT) void moe_decode_kernel(DecodeParams p) 
   const int b = blockIdx.x;
   if (b == 0) {
     decode_route<NSEG>(p, lds);
-    if (threadIdx.x == 0) decode_exit(p);
   } else if (b <= p.n_g1) {
     decode_gemm<true>(p, b - 1, lds, s_msg);
   } else {
@@ -2835,7 +2870,6 @@ hipError_t launch_decode(const void* x, const void* w_router, const uint8_t* val
   p.wait_limit = gt.site == MEP_GIVEUP_CHUNK ? gt.polls : sched::kWaitLimit;
   p.route_wait_limit = gt.site == MEP_GIVEUP_ROUTED ? gt.polls : sched::kWaitLimit;
   p.dbg_routed = gt.site == MEP_GIVEUP_ROUTED ? 0 : -1;
-  p.rec = reinterpret_cast<uint64_t*>(tile_queue + dec::kRec(hidden));
   const dim3 grid(static_cast<unsigned>(1 + p.n_g1 + p.n_g2));
   switch (hidden) {
     case 1024: moe_decode_kernel<1><<<grid, skinny::NT, 0, stream>>>(p); break;
