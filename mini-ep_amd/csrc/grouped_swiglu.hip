@@ -505,11 +505,14 @@ static_assert(BPW == NF, "one DMA block per MFMA group of an odd step");
 }  // namespace bfk
 
 // Words of the bf16 tiled kernels' schedule buffer (`tile_queue` of the C ABI,
-// int32, sched::words(max_rows, n_local) of them):
-//   [0, 8)           items taken from each XCD's queue
-//   8                workgroups finished
-//   9                items computed
-//   10               error flags, sticky (never cleared by a launch;
+// int32, sched::words(max_rows, n_local) of them).  Each word that many
+// workgroups update has a 128-byte line of its own (index x kLine): device-
+// scope atomics on one line are performed one after another where the line
+// lives, so counters sharing a line queue behind each other's traffic.
+//   line q < 8       items taken from XCD q's queue
+//   line 8           workgroups finished
+//   line 9           items computed
+//   line 10          error flags, sticky (never cleared by a launch;
 //                    mep_experts_check reads and clears them):
 //                    kFlagWait  a GEMM-2 tile gave up waiting for its rows
 //                               (or the combine for GEMM-2's); its
@@ -517,25 +520,30 @@ static_assert(BPW == NF, "one DMA block per MFMA group of an odd step");
 //                    kFlagDrain items computed != items listed (never expected)
 //                    kFlagInput offsets[n_local] < 0: the dispatch gave up,
 //                               no tile ran
-//   11               bit per drained queue
-//   12, 13           small-batch launch ending with the combine: GEMM-2
+//   line 11          bit per drained queue
+//   lines 12, 13     small-batch launch ending with the combine: GEMM-2
 //                    workgroups done, combine workgroups past their wait
-//   [16, 16 + RT)    GEMM-1 column tiles finished per row tile (kModeBoth)
-// Every launch leaves every word but 10 zero.
+//   line 16 + r      row tile r's GEMM-1 column tiles finished (kModeBoth);
+//                    the small-batch launch of both GEMMs: chunk r's GEMM-1
+//                    counts and GEMM-2 workgroups past their wait (words 0, 1)
+// Every launch leaves every word but the flags zero.
 namespace sched {
-constexpr int kQueue = 0, kDone = 8, kItems = 9, kFlags = 10, kDrained = 11, kG2Done = 12, kCombDone = 13,
-              kRowDone = 16;
+constexpr int kLine = 32;                      // ints per 128-byte line
+constexpr int kQueue = 0, kDone = 8 * kLine, kItems = 9 * kLine, kFlags = 10 * kLine, kDrained = 11 * kLine,
+              kG2Done = 12 * kLine, kCombDone = 13 * kLine, kRowDone = 16 * kLine;
+__host__ __device__ constexpr int queue_word(int q) { return kQueue + q * kLine; }
+__host__ __device__ constexpr int row_word(int r) { return kRowDone + r * kLine; }
 constexpr int kFlagWait = 1, kFlagDrain = 2, kFlagInput = kFlagInputBit;
 constexpr int kWaitLimit = 1 << 20;            // polls of one row counter (about a second)
 // the small-batch launch of both GEMMs runs up to this many rows
 constexpr int64_t kSmallRows = 1024;
 // row tiles of max_rows rows over n_local experts: each expert adds at most
-// one partial tile; the small-batch launch of both GEMMs keeps two words per
+// one partial tile; the small-batch launch of both GEMMs keeps a line per
 // 32-row chunk there instead
 inline int64_t words(int64_t max_rows, int n_local) {
   const int64_t tiles = (max_rows + 255) / 256 + n_local;
   const int64_t chunks = max_rows <= kSmallRows ? (max_rows + 31) / 32 + n_local : 0;
-  return kRowDone + (tiles > 2 * chunks ? tiles : 2 * chunks);
+  return kRowDone + (tiles > chunks ? tiles : chunks) * kLine;
 }
 }  // namespace sched
 
@@ -706,7 +714,7 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(MoeParams p) {
   const int q = static_cast<int>(blockIdx.x) & (nq - 1);
   const int n_static = static_cast<int>(gridDim.x) / nq;   // the grid is a multiple of nq
   const int first_pos = static_cast<int>(blockIdx.x) / nq;
-  auto claim = [&](int qq) { return n_static + atomic_add_1(sched + sched::kQueue + qq, 1); };
+  auto claim = [&](int qq) { return n_static + atomic_add_1(sched + sched::queue_word(qq), 1); };
 
   // ---- row tiles ------------------------------------------------------------------
   // offsets[nl] < 0: the dispatch gave up (its outputs are poisoned); then no
@@ -783,7 +791,7 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(MoeParams p) {
   // returns 1 if the wait gave up (the tile then stores NaN)
   auto wait_rows = [&](int R) {
     int polls = 0;
-    while (atomic_read(sched + sched::kRowDone + R) < need(R)) {
+    while (atomic_read(sched + sched::row_word(R)) < need(R)) {
       if (++polls == p.wait_limit) {
         atomic_or_1(sched + sched::kFlags, sched::kFlagWait);
         return 1;
@@ -1125,7 +1133,7 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(MoeParams p) {
     // loop: count the last GEMM-1 tile, then take two items
     __syncthreads();
     if (tid == 0) {
-      if (BOTH && sig_r >= 0) atomic_add_1(sched + sched::kRowDone + sig_r, 1);
+      if (BOTH && sig_r >= 0) atomic_add_1(sched + sched::row_word(sig_r), 1);
       int a = INT_MAX, b = INT_MAX, qq = cq;
       bool claimed = false;
       if (first_round) {
@@ -1233,12 +1241,12 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(MoeParams p) {
       if (it > 0 && has_next) rowmap_dma(nxt, (it + 1) & 1);
       // every wave waited for its stores (vmcnt(0)) before the barrier that
       // ended step 0: the previous GEMM-1 tile's act rows are complete
-      if (BOTH && tid == 0 && sig_r >= 0) atomic_add_1(sched + sched::kRowDone + sig_r, 1);
+      if (BOTH && tid == 0 && sig_r >= 0) atomic_add_1(sched + sched::row_word(sig_r), 1);
       sig_r = -1;
       int got = INT_MAX, dep = 0;
       if (tid == 0 && early) {
         if (ahead2 || ahead1) got = claim(cq);
-        if (poll) dep = atomic_read(sched + sched::kRowDone + nxt.R);
+        if (poll) dep = atomic_read(sched + sched::row_word(nxt.R));
       }
       step(S1, NO, YES, YES, sc, 2, 0, 1, act);          // step 1: DMA stage 2 -> buffer 0
       step(S0, NO, NO, YES, sc, 0, 0, 1, act);           // step 2 (stage 1)
@@ -1252,14 +1260,14 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(MoeParams p) {
         const bool late = k4 == KT - 8;
         if (tid == 0 && late) {
           if (ahead2 || ahead1) got = claim(cq);
-          if (poll) dep = atomic_read(sched + sched::kRowDone + nxt.R);
+          if (poll) dep = atomic_read(sched + sched::row_word(nxt.R));
         }
         step(S0, NO, NO, YES, sc, 0, 0, 0, act);
         // the claim came back before the barrier of step KT-8: a GEMM-2 tile
         // claimed for next polls its row tile (the row tile is arithmetic)
         if (BOTH && tid == 0 && late && ahead1) {
           const int nr = q_lo(cq + 1) - q_lo(cq);
-          if (got < n_items && got >= nr * n1) dep = atomic_read(sched + sched::kRowDone + q_lo(cq) + (got - nr * n1) / n2);
+          if (got < n_items && got >= nr * n1) dep = atomic_read(sched + sched::row_word(q_lo(cq) + (got - nr * n1) / n2));
         }
         step(S1, NO, YES, YES, sc, k4 / 2 + 2, 0, 1, act);
         step(S0, NO, NO, YES, sc, 0, 0, 1, act);
@@ -1323,7 +1331,7 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(MoeParams p) {
         __builtin_amdgcn_s_waitcnt(kVmcnt0);
         __syncthreads();
         if (tid == 0) {
-          if (BOTH && sig_r >= 0) atomic_add_1(sched + sched::kRowDone + sig_r, 1);
+          if (BOTH && sig_r >= 0) atomic_add_1(sched + sched::row_word(sig_r), 1);
           s_msg[4] = (BOTH && !cur.g1) ? wait_rows(cur.R) : 0;
         }
         sig_r = -1;
@@ -1354,13 +1362,13 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(MoeParams p) {
   if (__builtin_amdgcn_readfirstlane(s_msg[3]) == static_cast<int>(gridDim.x) - 1) {
     if (tid == 0) {
       if (atomic_read(sched + sched::kItems) != RT * per_row) atomic_or_1(sched + sched::kFlags, sched::kFlagDrain);
-      for (int j = 0; j < 8; ++j) atomicExch(sched + sched::kQueue + j, 0);
+      for (int j = 0; j < 8; ++j) atomicExch(sched + sched::queue_word(j), 0);
       atomicExch(sched + sched::kItems, 0);
       atomicExch(sched + sched::kDrained, 0);
       atomicExch(sched + sched::kDone, 0);
     }
     if (BOTH)
-      for (int r = tid; r < RT; r += NT) atomicExch(sched + sched::kRowDone + r, 0);
+      for (int r = tid; r < RT; r += NT) atomicExch(sched + sched::row_word(r), 0);
   }
 }
 
@@ -1540,7 +1548,7 @@ __device__ __forceinline__ void skinny_body(const GemmParams& p, int block, int 
   const T* A = static_cast<const T*>(p.A);
   T* const C = static_cast<T*>(p.C);
   // chunk counters of the fused launch: GEMM-1 workgroups done, GEMM-2 workgroups past the wait
-  int* const done1 = FUSED ? sched + sched::kRowDone + 2 * q : nullptr;
+  int* const done1 = FUSED ? sched + sched::row_word(q) : nullptr;
   int* const seen2 = FUSED ? done1 + 1 : nullptr;
 
   {
@@ -1893,15 +1901,15 @@ constexpr int E = 32;
 // behind them.
 constexpr int kPoison = sched::kRowDone;                // a routing wait gave up
 constexpr int kCombined = kPoison + 1;                  // column blocks combined
-constexpr int kBlock = 64;                              // ints per counter block
+constexpr int kBlock = 2 * sched::kLine;                // ints per counter block
 // expert e's block: GEMM-1 count, GEMM-2 workgroups past their wait, users
 // done with the routing record, and the record itself (one 64-bit word: bit
 // 63 set once written, bits 32..47 the expert's first row, bits 0..31 its
 // tokens, bit t for token t)
-__host__ __device__ constexpr int kExp(int e) { return kBlock * (1 + e); }
+__host__ __device__ constexpr int kExp(int e) { return sched::kRowDone + kBlock * (1 + e); }
 constexpr int kDone1 = 0, kSeen2 = 1, kUsers = 2, kRecWord = 4;
 // column block cb's block: GEMM-2 workgroups done with it
-__host__ __device__ constexpr int kColBlk(int cb) { return kBlock * (1 + E + cb); }
+__host__ __device__ constexpr int kColBlk(int cb) { return sched::kRowDone + kBlock * (1 + E + cb); }
 constexpr uint64_t kRecValid = 1ull << 63;
 constexpr int kRouterLds = E * kRowStride32 + kWaves * kRowsPerWave * (E + 1) * 4 + kWaves * E * 4 + 2 * E * 4;
 constexpr int kLds = kRouterLds > skinny::LDS_W ? kRouterLds : skinny::LDS_W;

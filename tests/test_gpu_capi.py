@@ -98,7 +98,7 @@ def test_error_codes_and_messages():
     # a tiled launch needs mep_experts_queue_ints words of schedule (checked before anything is enqueued)
     big = torch.zeros(9 << 20, dtype=torch.int32, device="cuda")     # 36 MiB: covers act of 32768 rows
     need = L.mep_experts_queue_ints(4096 * 8, 32)
-    assert need == 16 + 4096 * 8 // 256 + 32
+    assert need == (16 + 4096 * 8 // 256 + 32) * 32      # one 128-byte line per counter
     rc = L.mep_grouped_swiglu(big.data_ptr(), 4096, 8, big.data_ptr(), big.data_ptr(), 32, 4096 * 8, big.data_ptr(),
                               big.data_ptr(), 1024, 512, 1, big.data_ptr(), big.data_ptr(), big.numel() * 4,
                               big.data_ptr(), need - 1, None)
