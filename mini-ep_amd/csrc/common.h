@@ -85,13 +85,18 @@ hipError_t launch_route_dispatch_fused(const void* x, const void* w, int64_t n, 
 // waiting for another's histogram row
 constexpr uint32_t kFlagBarrier = 8u;
 
-// Header of a dispatch workspace: four 128-byte lines, then the status flags.
+// Header of a dispatch workspace: 128-byte lines, then the status flags.
 // Word 0: the number of launched blocks; kEpochWord: the epoch of the
-// one-launch exchange (its tags); kDoneWord: workgroups of the current
-// one-launch call that have finished; kGiveupWord: nonzero once one of them
-// gave up waiting.  The last two are zero between calls.
-constexpr int kWsHeaderBytes = 512;
-constexpr int kEpochWord = 32, kDoneWord = 64, kGiveupWord = 96;
+// one-launch exchange (its tags); kDoneWord: groups of workgroups of the
+// current one-launch call that have finished; kGiveupWord: nonzero once one
+// of them gave up waiting; line 4 + g: workgroups of group g that have
+// finished.  All but the first two are zero between calls.  (Each counter
+// has a line of its own: device-scope atomics on one line are performed one
+// after another, and a few hundred workgroups counting on one word would
+// queue for microseconds.)
+constexpr int kEpochWord = 32, kDoneWord = 64, kGiveupWord = 96, kGroupDoneWord = 128;
+constexpr int kMaxDoneGroups = 64;
+constexpr int kWsHeaderBytes = 4 * kGroupDoneWord + kMaxDoneGroups * 128;
 
 // row_of_entry value of an entry of a one-launch dispatch that gave up (a
 // workgroup waited too long for another's counts): the call's placement is
@@ -109,9 +114,12 @@ GiveupTest giveup_test();
 
 // End of a workgroup of a one-launch dispatch exchange, called by every lane
 // of wave 0 after a barrier that follows all of the workgroup's stores.  Lane
-// 0 records a give-up in the header, then counts the workgroup finished.  The
-// last workgroup of the call to finish (by then every other one has read the
-// epoch and completed its stores) returns both words to zero and gets
+// 0 records a give-up in the header, then counts the workgroup finished in
+// its group's word (groups of at least 16 consecutive blocks, at most
+// kMaxDoneGroups of them); the group's last workgroup returns that word to
+// zero and counts the group finished.  The last workgroup of the call to
+// finish (by then every other one has read the epoch and completed its
+// stores) returns the count and the give-up word to zero and gets
 // kExchangeLast, plus kExchangeGaveUp if any workgroup gave up; the others
 // get 0.  Only the last workgroup may advance the epoch: a workgroup that was
 // not resident with the others can start after the early ones have exited,
@@ -122,12 +130,19 @@ __device__ __forceinline__ int finish_exchange(uint32_t* header, bool gave_up, i
   if ((threadIdx.x & 63) == 0) {
     if (gave_up) __hip_atomic_fetch_or(header + kGiveupWord, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): the give-up is recorded before the count
-    const uint32_t done =
-        __hip_atomic_fetch_add(header + kDoneWord, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (done == static_cast<uint32_t>(n_blocks - 1)) {
-      const uint32_t g = __hip_atomic_exchange(header + kGiveupWord, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(header + kDoneWord, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      r = kExchangeLast | (g != 0u ? kExchangeGaveUp : 0);
+    const int per = max(16, (n_blocks + kMaxDoneGroups - 1) / kMaxDoneGroups);
+    const int g = static_cast<int>(blockIdx.x) / per, n_groups = (n_blocks + per - 1) / per;
+    uint32_t* const gw = header + kGroupDoneWord + 32 * g;
+    const uint32_t in_g = __hip_atomic_fetch_add(gw, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (in_g == static_cast<uint32_t>(min(per, n_blocks - g * per) - 1)) {
+      __hip_atomic_store(gw, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const uint32_t done =
+          __hip_atomic_fetch_add(header + kDoneWord, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (done == static_cast<uint32_t>(n_groups - 1)) {
+        const uint32_t gu = __hip_atomic_exchange(header + kGiveupWord, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(header + kDoneWord, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        r = kExchangeLast | (gu != 0u ? kExchangeGaveUp : 0);
+      }
     }
   }
   return __shfl(r, 0, 64);

@@ -159,12 +159,14 @@ __global__ __launch_bounds__(kWaves * 64) void router32_kernel(const uint16_t* _
 // them by flat entry id per expert inside the block (a token's 8 experts are
 // distinct, so an entry's rank is the number of earlier tokens of the block
 // that chose the same expert: wave ballots over the 5 id bits, then the waves'
-// counts in order) and publishes its histogram row.  From every workgroup's
-// row it takes the expert totals (counts, offsets) and its own prefix over
-// earlier blocks, which place every entry:
+// counts in order) and publishes its histogram row.  The expert totals
+// (counts, offsets) and each block's prefix over earlier blocks place every
+// entry:
 //   row = offsets[e] + #(e in earlier blocks) + #(e earlier in this block),
-// the stable grouping by expert of modeling.py:94-96.  Results equal
-// router32_kernel followed by the dispatch's scatter_kernel bit for bit.
+// the stable grouping by expert of modeling.py:94-96: every workgroup reads
+// every row (8 words of four 8-bit counts, 64 bytes) and takes the totals
+// and its prefix over earlier blocks.  Results equal router32_kernel followed
+// by the dispatch's scatter_kernel bit for bit.
 //
 // Every workgroup must be resident at once (the host launches at most as
 // many as the device holds).  There is no counter and no atomic: each row
@@ -172,8 +174,8 @@ __global__ __launch_bounds__(kWaves * 64) void router32_kernel(const uint16_t* _
 // (sc1) accesses, so a word written on one XCD is read fresh on every other,
 // and a workgroup re-reads the words whose tag is not yet this call's.  The
 // tag is 2^31 | (the workspace's epoch word + 1): every workgroup reads the
-// epoch as it starts, and workgroup 0 advances it once it has seen every row
-// of this call (by then every workgroup has read it).  Words of earlier calls
+// epoch as it starts, and the last workgroup to finish advances it (by then
+// every workgroup has read it).  Words of earlier calls
 // carry older tags, and whatever else the library leaves in a workspace
 // (counts, flags, table entries: small non-negative values) has a clear top
 // bit, so the workspace must only be zero-filled once before its first use
@@ -181,8 +183,8 @@ __global__ __launch_bounds__(kWaves * 64) void router32_kernel(const uint16_t* _
 // kFlagBarrier in the block's status word: the workgroup places nothing (its
 // entries get kPoisonRow), every workgroup exits, the last one to finish
 // poisons the whole call (finish_exchange) and mep_dispatch_check reports it.
-// The last workgroup to finish also advances the epoch.
 constexpr int kRowPolls = 1 << 20;
+constexpr int kRowWords = 8;                      // 64-bit words of a histogram row: 4 counts each
 
 struct FusedDispatch {
   int32_t* counts;          // (E,) rows per expert
@@ -190,7 +192,7 @@ struct FusedDispatch {
   int32_t* perm;            // (N k,) perm[row] = flat entry id
   int32_t* row_of_entry;    // (N k,) row of each entry, -1 for masked tokens
   int64_t* route_counts;    // (E,) += entries per expert, or NULL
-  uint64_t* rows;           // (n_blocks, E) tagged histogram rows
+  uint64_t* rows;           // (n_blocks, kRowWords) tagged histogram rows
   uint32_t* header;         // [0] = n_blocks; [kEpochWord]: the epoch
   uint32_t* flags;          // (2 n_blocks,) status words: count pass (0), scatter pass
   const uint8_t* valid;     // (N,) or NULL
@@ -276,22 +278,32 @@ __global__ __launch_bounds__(kWaves * 64) void route_dispatch32_kernel(const uin
     s_part[part][0][e] = 0;
     s_part[part][1][e] = c;
   } else {
-    if (tid < E && b != o.withhold) {
-      int c = 0;
+    // the row as kRowWords words: tag | four 8-bit counts (a block has at
+    // most 64 tokens, so a count fits)
+    if (tid < kRowWords && b != o.withhold) {
+      uint32_t packed = 0u;
 #pragma unroll
-      for (int ww = 0; ww < kWaves; ++ww) c += s_wcnt[ww][tid];
-      store_dev(o.rows + static_cast<int64_t>(b) * E + tid, tag | static_cast<uint32_t>(c));
+      for (int q = 0; q < 4; ++q) {
+        int c = 0;
+#pragma unroll
+        for (int ww = 0; ww < kWaves; ++ww) c += s_wcnt[ww][4 * tid + q];
+        packed |= static_cast<uint32_t>(c) << (8 * q);
+      }
+      store_dev(o.rows + static_cast<int64_t>(b) * kRowWords + tid, tag | packed);
     }
-    const int e = tid % E, part = tid / E;
-    int pre = 0, tot = 0;
+    // every block's row: thread (word j, part) reads rows part + 32 u of word
+    // j, re-reading each until it carries this call's tag
+    constexpr int kPartsW = kWaves * 64 / kRowWords;
+    const int j = tid % kRowWords, part = tid / kRowWords;
+    int pre[4] = {0, 0, 0, 0}, tot[4] = {0, 0, 0, 0};
     uint32_t bad = 0u;
-    constexpr int kBatch = 32;
-    for (int bb0 = part; bb0 < nb; bb0 += kParts * kBatch) {
+    constexpr int kBatch = 8;
+    for (int bb0 = part; bb0 < nb; bb0 += kPartsW * kBatch) {
       uint64_t v[kBatch];
 #pragma unroll
       for (int u = 0; u < kBatch; ++u) {
-        const int bb = bb0 + u * kParts;
-        v[u] = bb < nb ? load_dev(o.rows + static_cast<int64_t>(bb) * E + e) : tag;
+        const int bb = bb0 + u * kPartsW;
+        v[u] = bb < nb ? load_dev(o.rows + static_cast<int64_t>(bb) * kRowWords + j) : tag;
       }
       for (int it = 0;; ++it) {
         bool stale = false;
@@ -302,19 +314,39 @@ __global__ __launch_bounds__(kWaves * 64) void route_dispatch32_kernel(const uin
         __builtin_amdgcn_s_sleep(1);
 #pragma unroll
         for (int u = 0; u < kBatch; ++u)
-          if ((v[u] & ~0xffffffffull) != tag) v[u] = load_dev(o.rows + static_cast<int64_t>(bb0 + u * kParts) * E + e);
+          if ((v[u] & ~0xffffffffull) != tag)
+            v[u] = load_dev(o.rows + static_cast<int64_t>(bb0 + u * kPartsW) * kRowWords + j);
       }
 #pragma unroll
       for (int u = 0; u < kBatch; ++u) {
-        const int bb = bb0 + u * kParts;
-        const int c = static_cast<int>(static_cast<uint32_t>(v[u]));
-        tot += c;
-        pre += bb < b ? c : 0;
+        const int bb = bb0 + u * kPartsW;
+        const uint32_t w = bb < nb ? static_cast<uint32_t>(v[u]) : 0u;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int c = static_cast<int>((w >> (8 * q)) & 0xffu);
+          tot[q] += c;
+          pre[q] += bb < b ? c : 0;
+        }
       }
     }
-    s_part[part][0][e] = pre;
-    s_part[part][1][e] = tot;
+    // the wave's parts of word j (lanes j, j + 8, ..., j + 56), then the waves'
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int d = kRowWords; d < 64; d <<= 1) {
+        pre[q] += __shfl_xor(pre[q], d, 64);
+        tot[q] += __shfl_xor(tot[q], d, 64);
+      }
+    if (lane < kRowWords)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        s_part[wave][0][4 * lane + q] = pre[q];
+        s_part[wave][1][4 * lane + q] = tot[q];
+      }
     if (bad) s_flag = bad;
+    if (tid < E)                                   // no part beyond the waves'
+#pragma unroll
+      for (int q = kWaves; q < kParts; ++q) s_part[q][0][tid] = s_part[q][1][tid] = 0;
   }
   __syncthreads();
   // a workgroup whose wait gave up has rows of earlier calls: it places

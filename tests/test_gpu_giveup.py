@@ -33,6 +33,7 @@ from miniep_amd import _lib, ops, workloads
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
 POLLS = 2000
+HEADER_BYTES = 512 + 64 * 128                                 # dispatch workspace header: 4 lines + 64 group lines
 
 
 @contextlib.contextmanager
@@ -90,7 +91,8 @@ def test_route_dispatch_giveup():
                                    "mep_route_dispatch"), "gave up")
     assert int(d1.offsets[-1]) == -1
     assert bool((d1.row_of_entry == -2).all())
-    assert int(words[64]) == 0 and int(words[96]) == 0      # finished-workgroup counter, give-up word
+    assert int(words[64]) == 0 and int(words[96]) == 0      # finished-group counter, give-up word
+    assert int(ws[512:HEADER_BYTES].view(torch.int32).abs().sum()) == 0   # per-group finished counters
     assert int(words[32]) == epoch + 1                      # advanced once, by the last workgroup
     assert torch.equal(idx1, idx0) and torch.equal(gate1, gate0)   # the router part is unaffected
     # downstream: no tile runs on the poisoned offsets, every output is NaN
@@ -144,6 +146,7 @@ def test_dispatch_giveup_ep_share():
     assert bool((d1.row_of_entry[: n * k] == -2).all())
     assert torch.equal(rr1, rr_init)                          # no block applied the counter update
     assert int(words[64]) == 0 and int(words[96]) == 0
+    assert int(ws[512:HEADER_BYTES].view(torch.int32).abs().sum()) == 0
     d2, rr2 = run(True)
     assert torch.equal(d2.offsets, d0.offsets) and torch.equal(d2.counts, d0.counts)
     m = int(d0.offsets[-1])
