@@ -657,6 +657,12 @@ __device__ __forceinline__ int atomic_read(int* p) {
   return atomicAdd(p + z, z);
 }
 __device__ __forceinline__ int atomic_or_1(int* p, int v) { return atomicOr(p + opaque_zero(), v); }
+// Device-scope 32-bit load (written earlier in this launch, possibly on
+// another XCD): what a wait polls, so that the counter's line only sees the
+// counting read-modify-writes.
+__device__ __forceinline__ int load_dev_i32(const int32_t* q) {
+  return __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // 16-byte store with device scope (sc1): written through to memory, where a
 // later read from another XCD finds it.  base / bytes as in buffer_lds_16.
@@ -791,7 +797,7 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(MoeParams p) {
   // returns 1 if the wait gave up (the tile then stores NaN)
   auto wait_rows = [&](int R) {
     int polls = 0;
-    while (atomic_read(sched + sched::row_word(R)) < need(R)) {
+    while (load_dev_i32(sched + sched::row_word(R)) < need(R)) {
       if (++polls == p.wait_limit) {
         atomic_or_1(sched + sched::kFlags, sched::kFlagWait);
         return 1;
@@ -1246,7 +1252,7 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(MoeParams p) {
       int got = INT_MAX, dep = 0;
       if (tid == 0 && early) {
         if (ahead2 || ahead1) got = claim(cq);
-        if (poll) dep = atomic_read(sched + sched::row_word(nxt.R));
+        if (poll) dep = load_dev_i32(sched + sched::row_word(nxt.R));
       }
       step(S1, NO, YES, YES, sc, 2, 0, 1, act);          // step 1: DMA stage 2 -> buffer 0
       step(S0, NO, NO, YES, sc, 0, 0, 1, act);           // step 2 (stage 1)
@@ -1260,14 +1266,14 @@ __global__ __launch_bounds__(bfk::NT) void moe_gemm_bf16_kernel(MoeParams p) {
         const bool late = k4 == KT - 8;
         if (tid == 0 && late) {
           if (ahead2 || ahead1) got = claim(cq);
-          if (poll) dep = atomic_read(sched + sched::row_word(nxt.R));
+          if (poll) dep = load_dev_i32(sched + sched::row_word(nxt.R));
         }
         step(S0, NO, NO, YES, sc, 0, 0, 0, act);
         // the claim came back before the barrier of step KT-8: a GEMM-2 tile
         // claimed for next polls its row tile (the row tile is arithmetic)
         if (BOTH && tid == 0 && late && ahead1) {
           const int nr = q_lo(cq + 1) - q_lo(cq);
-          if (got < n_items && got >= nr * n1) dep = atomic_read(sched + sched::row_word(q_lo(cq) + (got - nr * n1) / n2));
+          if (got < n_items && got >= nr * n1) dep = load_dev_i32(sched + sched::row_word(q_lo(cq) + (got - nr * n1) / n2));
         }
         step(S1, NO, YES, YES, sc, k4 / 2 + 2, 0, 1, act);
         step(S0, NO, NO, YES, sc, 0, 0, 1, act);
@@ -1591,7 +1597,7 @@ __device__ __forceinline__ void skinny_body(const GemmParams& p, int block, int 
     auto wait_count = [&](int target) {
       if (q == p.dbg_chunk) ++target;
       int polls = 0;
-      while (atomic_read(done1) < target) {
+      while (load_dev_i32(done1) < target) {
         if (++polls == p.wait_limit) {
           atomic_or_1(sched + sched::kFlags, sched::kFlagWait);
           *s_gave = 1;
@@ -1755,7 +1761,7 @@ __device__ void skinny_combine(const CombineParams& cp, const uint16_t* y, int c
   if (tid == 0) {
     int polls = 0, gave = 0;
     const int target = cp.n_g2 + (cb == cp.dbg_comb ? 1 : 0);
-    while (atomic_read(sched + sched::kG2Done) < target) {
+    while (load_dev_i32(sched + sched::kG2Done) < target) {
       if (++polls == cp.wait_limit) {
         atomic_or_1(sched + sched::kFlags, sched::kFlagWait);
         gave = 1;
@@ -1943,10 +1949,6 @@ struct DecodeParams {
   int dbg_routed;                // GEMM-1 workgroup whose routing wait cannot end (test hook; -1: none)
 };
 
-// Device-scope 32-bit load (written earlier in this launch, possibly on another XCD).
-__device__ __forceinline__ int load_dev_i32(const int32_t* q) {
-  return __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 // A user of expert e's routing record is done with it (workgroup 0 after
 // writing it, every GEMM-1 and GEMM-2 workgroup of the expert after reading
@@ -2427,7 +2429,12 @@ __global__ __launch_bounds__(skinny::NT) void moe_decode_kernel(DecodeParams p) 
   __shared__ int s_msg[4];
   const int b = blockIdx.x;
   if (b == 0) {
+    // the routing, then the last GEMM-2 unit (its weights are needed only
+    // once GEMM-1 is done): the grid is then one workgroup smaller, and at
+    // hidden 1024 every workgroup is resident from the start (two per CU)
     decode_route<NSEG>(p, lds);
+    __syncthreads();                                 // the router's LDS is free
+    decode_gemm<false>(p, p.n_g2 - 1, lds, s_msg);
   } else if (b <= p.n_g1) {
     decode_gemm<true>(p, b - 1, lds, s_msg);
   } else {
@@ -2878,7 +2885,7 @@ hipError_t launch_decode(const void* x, const void* w_router, const uint8_t* val
   p.wait_limit = gt.site == MEP_GIVEUP_CHUNK ? gt.polls : sched::kWaitLimit;
   p.route_wait_limit = gt.site == MEP_GIVEUP_ROUTED ? gt.polls : sched::kWaitLimit;
   p.dbg_routed = gt.site == MEP_GIVEUP_ROUTED ? 0 : -1;
-  const dim3 grid(static_cast<unsigned>(1 + p.n_g1 + p.n_g2));
+  const dim3 grid(static_cast<unsigned>(p.n_g1 + p.n_g2));   // workgroup 0 also runs GEMM-2 unit n_g2 - 1
   switch (hidden) {
     case 1024: moe_decode_kernel<1><<<grid, skinny::NT, 0, stream>>>(p); break;
     case 2048: moe_decode_kernel<2><<<grid, skinny::NT, 0, stream>>>(p); break;
