@@ -1593,11 +1593,14 @@ __device__ __forceinline__ void skinny_body(const GemmParams& p, int block, int 
       for (int f = 0; f < MFC; ++f) cell[f] = p.perm[min(r0 + 16 * f + lr, row_hi - 1)];
     }
     // thread 0: until the chunk's counter reaches `target` (one more for the
-    // test hook's chunk); a give-up sets the wait flag and *s_gave
+    // test hook's chunk); a give-up sets the wait flag and *s_gave.  Polled
+    // with read-modify-writes: polled with device-scope loads (here and in
+    // the combine's wait below) the two-launch decode layer took 38.6 us
+    // instead of 33.6 (same box, alternating builds)
     auto wait_count = [&](int target) {
       if (q == p.dbg_chunk) ++target;
       int polls = 0;
-      while (load_dev_i32(done1) < target) {
+      while (atomic_read(done1) < target) {
         if (++polls == p.wait_limit) {
           atomic_or_1(sched + sched::kFlags, sched::kFlagWait);
           *s_gave = 1;
@@ -1761,7 +1764,7 @@ __device__ void skinny_combine(const CombineParams& cp, const uint16_t* y, int c
   if (tid == 0) {
     int polls = 0, gave = 0;
     const int target = cp.n_g2 + (cb == cp.dbg_comb ? 1 : 0);
-    while (load_dev_i32(sched + sched::kG2Done) < target) {
+    while (atomic_read(sched + sched::kG2Done) < target) {
       if (++polls == cp.wait_limit) {
         atomic_or_1(sched + sched::kFlags, sched::kFlagWait);
         gave = 1;
