@@ -37,23 +37,27 @@ def _queue_words_zero():
         assert int(q.abs().sum()) == 0
 
 
-def _layer(n, seed, hidden=1024):
-    L = workloads.make_layer(n, seed=seed, hidden=hidden)
+def _layer(n, seed, hidden=1024, inter=512):
+    L = workloads.make_layer(n, seed=seed, hidden=hidden, inter=inter)
     return (L.x.to(BF).to(DEV), L.w_router.to(BF).to(DEV), L.w_in.to(BF).to(DEV), L.w_out.to(BF).to(DEV), L)
 
 
-@pytest.mark.parametrize("case", ["t1", "t7", "t16", "t32", "masked_t32", "h2048_t24", "t33"])
+@pytest.mark.parametrize("case", ["t1", "t7", "t16", "t32", "masked_t32", "h2048_t24", "h4096_t8", "i1024_t32", "t33"])
 def test_moe_layer_equals_two_calls(case):
+    """Shapes: hidden 1024 / 2048 / 4096 (GEMM-1's K loop of 4 / 8 / 16
+    blocks of x through the LDS ring), intermediate 1024 (GEMM-2 has K-steps
+    past the 16 it stages), masks, and 33 tokens (the two calls)."""
     banner(f"moe_layer one launch vs two calls: {case}")
     n = int(case.split("_t")[-1].lstrip("t"))
-    hidden = 2048 if case.startswith("h2048") else 1024
-    x, w_r, wi, wo, L = _layer(n, 61 + n, hidden)
+    hidden = {"h2048": 2048, "h4096": 4096}.get(case.split("_")[0], 1024)
+    inter = 1024 if case.startswith("i1024") else 512
+    x, w_r, wi, wo, L = _layer(n, 61 + n, hidden, inter)
     g = torch.Generator().manual_seed(n)
     valid = (torch.rand(n, generator=g) < 0.6).to(DEV) if case.startswith("masked") else None
     rc1 = torch.zeros(32, dtype=torch.int64, device=DEV)
     rc2 = torch.zeros(32, dtype=torch.int64, device=DEV)
     for rep in range(2):                                     # a second input through the same buffers
-        xr = x if rep == 0 else torch.randn(x.shape, generator=g).to(BF).to(DEV)
+        xr = x if rep == 0 else torch.randn(tuple(x.shape), generator=g).to(BF).to(DEV)
         got = ops.moe_layer(xr, w_r, 8, wi, wo, valid, route_counts=rc1, return_logits=True)
         ops.experts_check()
         ops.dispatch_check()
