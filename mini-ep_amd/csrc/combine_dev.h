@@ -35,13 +35,16 @@ __device__ __forceinline__ u32x4 pack_row_chunk(const float* acc) {
 }
 
 // DEV: the token's row_of_entry entries and gates are read with device-scope
-// loads (written earlier in the same launch, possibly on another XCD).
+// loads (written earlier in the same launch, possibly on another XCD), and so
+// is `poison` if given: nonzero there makes the chunk NaN, as a poisoned
+// entry does (one more load issued with the others, not a round trip before).
 template <int DT, class LoadY, bool DEV = false>
 __device__ __forceinline__ void combine8_chunk(const typename Elem<DT>::T* __restrict__ y,
                                                const typename Elem<DT>::T* __restrict__ gate,
                                                const int32_t* __restrict__ row_of_entry,
                                                const uint8_t* __restrict__ valid, int64_t t, int c, int hidden,
-                                               typename Elem<DT>::T* __restrict__ out, LoadY load_y) {
+                                               typename Elem<DT>::T* __restrict__ out, LoadY load_y,
+                                               const int32_t* poison_word = nullptr) {
   typedef typename Elem<DT>::T T;
   constexpr int K = 8;
   constexpr int EPC = 16 / Elem<DT>::kBytes;
@@ -51,7 +54,9 @@ __device__ __forceinline__ void combine8_chunk(const typename Elem<DT>::T* __res
   for (int s = 0; s < K; ++s) v[s] = load_y(ybase + static_cast<int64_t>(s) * hidden);
   int32_t row[K];
   float g[K];
+  int32_t pw = 0;
   if constexpr (DEV) {
+    if (poison_word != nullptr) pw = __hip_atomic_load(poison_word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     static_assert(DT == MEP_DTYPE_BF16, "device-scope reads of bf16 gates");
     const uint64_t* rp = reinterpret_cast<const uint64_t*>(row_of_entry + t * K);
     const uint64_t* gp = reinterpret_cast<const uint64_t*>(gate + t * K);
@@ -75,7 +80,7 @@ __device__ __forceinline__ void combine8_chunk(const typename Elem<DT>::T* __res
     }
   }
   const bool tok_ok = valid == nullptr || valid[t] != 0;
-  bool poison = false;
+  bool poison = pw != 0;
   float acc[EPC];
 #pragma unroll
   for (int q = 0; q < EPC; ++q) acc[q] = 0.0f;

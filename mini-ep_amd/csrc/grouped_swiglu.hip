@@ -2068,7 +2068,9 @@ __device__ void decode_route(const DecodeParams& p, unsigned char* lds) {
 
 // The last GEMM-2 workgroup of column block cb: out[t, cb*128 .. +128) for
 // every token, combine8's slot-order sum with device-scope reads of y, the
-// gates and row_of_entry; NaN everywhere if a routing wait gave up.  It then
+// gates and row_of_entry; NaN everywhere if a routing wait gave up (the
+// poison word is read with the other loads, after this workgroup's count of
+// the column block returned, so after every GEMM-2 count it follows).  It then
 // counts the column block combined; the last column block returns the
 // poison and its own counter to zero.
 __device__ void decode_combine(const DecodeParams& p, int cb, int n_cb2, int* s_msg) {
@@ -2076,19 +2078,12 @@ __device__ void decode_combine(const DecodeParams& p, int cb, int n_cb2, int* s_
   const uint16_t* const y = static_cast<const uint16_t*>(p.g2.C);
   const int H = p.g2.N;
   const uint32_t y_bytes = static_cast<uint32_t>(p.n_tokens * 8 * H * 2);
-  if (tid == 0) s_msg[2] = atomic_read(p.sched + dec::kPoison);
-  __syncthreads();
-  const bool poison = __builtin_amdgcn_readfirstlane(s_msg[2]) != 0;
   for (int q = tid; q < p.n_tokens * 16; q += skinny::NT) {
     const int64_t t = q >> 4;
     const int c = cb * 16 + (q & 15);
-    if (poison) {
-      const uint32_t nan2 = pack_bf16x2(__builtin_nanf(""), __builtin_nanf(""));
-      *reinterpret_cast<u32x4*>(p.out + t * H + c * 8) = u32x4{nan2, nan2, nan2, nan2};
-    } else {
-      auto ld = [&](const uint16_t* ptr) { return load_dev_16(y, y_bytes, static_cast<uint32_t>((ptr - y) * 2)); };
-      combine8_chunk<MEP_DTYPE_BF16, decltype(ld), true>(y, p.gate, p.row_of_entry, p.valid, t, c, H, p.out, ld);
-    }
+    auto ld = [&](const uint16_t* ptr) { return load_dev_16(y, y_bytes, static_cast<uint32_t>((ptr - y) * 2)); };
+    combine8_chunk<MEP_DTYPE_BF16, decltype(ld), true>(y, p.gate, p.row_of_entry, p.valid, t, c, H, p.out, ld,
+                                                       p.sched + dec::kPoison);
   }
   if (tid == 0 && atomic_add_1(p.sched + dec::kCombined, 1) == n_cb2 - 1) {
     atomic_add_1(p.sched + dec::kCombined, -n_cb2);
