@@ -2073,7 +2073,7 @@ __device__ void decode_route(const DecodeParams& p, unsigned char* lds) {
 // the column block returned, so after every GEMM-2 count it follows).  It then
 // counts the column block combined; the last column block returns the
 // poison and its own counter to zero.
-__device__ void decode_combine(const DecodeParams& p, int cb, int n_cb2, int* s_msg) {
+__device__ void decode_combine(const DecodeParams& p, int cb, int n_cb2) {
   const int tid = threadIdx.x;
   const uint16_t* const y = static_cast<const uint16_t*>(p.g2.C);
   const int H = p.g2.N;
@@ -2232,7 +2232,7 @@ __device__ void decode_gemm(const DecodeParams& p, int u, unsigned char* lds, in
       // no rows: nothing to compute (every token masked: expert 0's GEMM-2
       // workgroups write the zero outputs)
       __builtin_amdgcn_s_waitcnt(kVmcnt0);        // no DMA may still be writing LDS when the waves end
-      if (n_active == 0 && e == 0) decode_combine(p, cb, n_cb2, s_msg);
+      if (n_active == 0 && e == 0) decode_combine(p, cb, n_cb2);
       return;
     }
   }
@@ -2362,7 +2362,7 @@ __device__ void decode_gemm(const DecodeParams& p, int u, unsigned char* lds, in
     // before t (checked, so that a record read after a give-up stays in bounds)
     uint32_t mask = static_cast<uint32_t>(rec) & (n >= 32 ? ~0u : (1u << n) - 1u);
     const int first = static_cast<int>((rec >> 32) & 0xFFFFu);
-    if (first + __popc(mask) > max_entries) mask = 0u;
+    if (first + static_cast<int>(__popc(mask)) > max_entries) mask = 0u;
 #pragma unroll
     for (int f = 0; f < MFC; ++f) {
       const int t = 16 * f + lr;
@@ -2417,7 +2417,7 @@ __device__ void decode_gemm(const DecodeParams& p, int u, unsigned char* lds, in
       if (c == n_active - 1) atomic_add_1(col, -n_active);
     }
     __syncthreads();
-    if (__builtin_amdgcn_readfirstlane(s_msg[1])) decode_combine(p, cb, n_cb2, s_msg);
+    if (__builtin_amdgcn_readfirstlane(s_msg[1])) decode_combine(p, cb, n_cb2);
   }
 }
 
