@@ -496,7 +496,7 @@ def main(argv=None) -> int:
         "combine": {"ms": stage_ms["combine"], "GB/s": combine_bytes / (stage_ms["combine"] / 1e3) / 1e9,
                     "frac_hbm": combine_bytes / (stage_ms["combine"] / 1e3) / PEAK_HBM_BYTES},
     }
-    # north-star figure: both GEMMs of the timed steps (one launch), algorithmic flops
+    # the headline GEMM figure: both GEMMs of the timed steps (one launch), algorithmic flops
     gemm_util = (flops_g1 + flops_g2) / (exp_ms / 1e3) / PEAK_BF16_FLOPS
     achieved = (flops_g1 + flops_g2) / (exp_ms / 1e3) / 1e12
     traffic = traffic_from_profile()
