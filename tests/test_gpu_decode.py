@@ -86,6 +86,28 @@ def test_moe_layer_equals_two_calls(case):
         assert (o[~v] == 0).all()
 
 
+def test_moe_layer_interleaved_with_large_dispatch():
+    """The decode launch and the one-launch router + dispatch of a large
+    batch share the stream's dispatch workspace (header, status words, the
+    epoch that tags the exchange) and schedule buffer: interleaved, each
+    gives the bits it gives alone."""
+    banner("moe_layer one launch interleaved with a 4096-token route_dispatch")
+    x, w_r, wi, wo, _ = _layer(32, 74)
+    L = workloads.make_layer(4096, seed=75, zipf_s=1.2)
+    xb, wb = L.x.to(BF).to(DEV), L.w_router.to(BF).to(DEV)
+    out0 = ops.moe_layer(x, w_r, 8, wi, wo)[0].clone()
+    idx0, gate0, d0 = ops.route_dispatch(xb, wb, 8, check=True)
+    ref = (idx0.clone(), d0.offsets.clone(), d0.perm.clone(), d0.row_of_entry.clone())
+    for _ in range(3):
+        out = ops.moe_layer(x, w_r, 8, wi, wo)[0]
+        idx, gate, d = ops.route_dispatch(xb, wb, 8, check=True)
+        ops.experts_check()
+        assert torch.equal(out, out0)
+        assert torch.equal(idx, ref[0]) and torch.equal(d.offsets, ref[1])
+        assert torch.equal(d.perm, ref[2]) and torch.equal(d.row_of_entry, ref[3])
+    _queue_words_zero()
+
+
 def test_moe_layer_every_token_masked():
     banner("moe_layer one launch: every token masked")
     x, w_r, wi, wo, _ = _layer(16, 71)
