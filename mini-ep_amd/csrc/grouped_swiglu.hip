@@ -1965,6 +1965,21 @@ __device__ __forceinline__ void decode_rec_done(const DecodeParams& p, int e) {
   }
 }
 
+// A GEMM-2 workgroup of expert e is done with the expert's GEMM-1 count
+// (past its wait, at its end): the last of the expert's GEMM-2 workgroups
+// takes the counts back out, so a count that arrives after a give-up still
+// leaves both at zero.  Counted at the end, next to the column block's
+// count, so that its round trip is not one more between GEMM-1's last count
+// and GEMM-2's K loop.
+__device__ __forceinline__ void decode_seen2(const DecodeParams& p, int e) {
+  int* const seen2 = p.sched + dec::kExp(e) + dec::kSeen2;
+  const int n_cb = p.g2.N / 128;
+  if (atomic_add_1(seen2, 1) == n_cb - 1) {
+    atomic_add_1(p.sched + dec::kExp(e) + dec::kDone1, -2 * (p.g1.N / 64));
+    atomic_add_1(seen2, -n_cb);
+  }
+}
+
 // Workgroup 0: route the batch (router32_logits, router_tail: the fused
 // router's code), dispatch it as one block (flat order, stable by expert:
 // modeling.py:94-96), then publish the routing.
@@ -2123,7 +2138,6 @@ __device__ void decode_gemm(const DecodeParams& p, int u, unsigned char* lds, in
   const T* wp0 = W + static_cast<int64_t>(wrow[0]) * K + 8 * lg;
   const T* wp1 = W + static_cast<int64_t>(wrow[1]) * K + 8 * lg;
   int* const done1 = sched + dec::kExp(e) + dec::kDone1;
-  int* const seen2 = sched + dec::kExp(e) + dec::kSeen2;
   uint64_t rec = 0;                                      // the expert's routing record
   auto load_rec = [&]() {
     return __hip_atomic_load(dec::rec_word(sched, e), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -2219,19 +2233,13 @@ __device__ void decode_gemm(const DecodeParams& p, int u, unsigned char* lds, in
         }
         __builtin_amdgcn_s_sleep(2);
       }
-      // the last GEMM-2 workgroup of the expert past the wait takes the
-      // counts back out (so a count that arrives after a give-up still
-      // leaves both at zero)
-      if (atomic_add_1(seen2, 1) == n_cb - 1) {
-        atomic_add_1(done1, -2 * n_cb1);
-        atomic_add_1(seen2, -n_cb);
-      }
     }
     __syncthreads();
     if (hi == lo) {
       // no rows: nothing to compute (every token masked: expert 0's GEMM-2
       // workgroups write the zero outputs)
       __builtin_amdgcn_s_waitcnt(kVmcnt0);        // no DMA may still be writing LDS when the waves end
+      if (tid == 0) decode_seen2(p, e);
       if (n_active == 0 && e == 0) decode_combine(p, cb, n_cb2);
       return;
     }
@@ -2413,6 +2421,7 @@ __device__ void decode_gemm(const DecodeParams& p, int u, unsigned char* lds, in
     if (tid == 0) {
       int* const col = sched + dec::kColBlk(cb);
       const int c = atomic_add_1(col, 1);
+      decode_seen2(p, e);                                  // its round trip overlaps the count's
       s_msg[1] = c == n_active - 1;
       if (c == n_active - 1) atomic_add_1(col, -n_active);
     }
