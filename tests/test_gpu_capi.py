@@ -6,7 +6,7 @@ import pytest
 import torch
 
 from helpers import banner
-from miniep_amd import HipMoEBackend, _lib, route, workloads
+from miniep_amd import HipMoEBackend, _lib, ops, route, workloads
 
 pytestmark = pytest.mark.gpu
 
@@ -80,6 +80,71 @@ def test_raw_ctypes_layer_matches_backend(n):
     ref = HipMoEBackend(w_in, w_out)(x, idx2, gate2)
     assert torch.equal(idx, idx2) and torch.equal(gate, gate2)
     assert torch.equal(out, ref) and torch.equal(out1, ref)
+
+
+class _RawBlock:
+    """The whole block through the raw C ABI (mep_moe_layer), with argtypes
+    of its own on a separate handle of the library, as a binding would
+    declare them; the dispatch workspace grows (zero-filled) with the batch
+    and the schedule buffer is kept per size, left zero by every call."""
+
+    def __init__(self):
+        vp, i32, i64, sz = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_size_t
+        L = ctypes.CDLL(_lib.lib()._name)
+        L.mep_last_error.restype = ctypes.c_char_p
+        L.mep_route_dispatch_workspace_size.restype = sz
+        L.mep_route_dispatch_workspace_size.argtypes = [i64, i32]
+        L.mep_moe_layer_queue_ints.restype = sz
+        L.mep_moe_layer_queue_ints.argtypes = [i64, i32, i32]
+        L.mep_experts_workspace_size.restype = sz
+        L.mep_experts_workspace_size.argtypes = [i64, i32, i32]
+        L.mep_moe_layer.restype = ctypes.c_int
+        L.mep_moe_layer.argtypes = [vp, vp, vp, i64, i32, i32, i32, i32, vp, vp, i32, vp, vp, vp,
+                                    vp, vp, vp, vp, vp, vp, vp, sz, vp, sz, vp, sz, vp, vp]
+        self.L, self.dws, self.queues = L, None, {}
+
+    def __call__(self, x, w_r, w_in, w_out, k=8):
+        L = self.L
+        N, H = x.shape
+        E, I = w_r.shape[0], w_out.shape[2]
+        s = torch.cuda.current_stream().cuda_stream
+        e = lambda *shape, dt=torch.int32: torch.empty(*shape, dtype=dt, device="cuda")
+        idx, gate = e(N, k, dt=torch.int64), e(N, k, dt=x.dtype)
+        counts, offsets, perm, row = e(E), e(E + 1), e(N * k), e(N * k)
+        y, out = e(N * k, H, dt=x.dtype), e(N, H, dt=x.dtype)
+        need = L.mep_route_dispatch_workspace_size(N, E)
+        if self.dws is None or self.dws.numel() < need:
+            self.dws = torch.zeros(need, dtype=torch.uint8, device="cuda")
+        act = e(L.mep_experts_workspace_size(N * k, I, 1), dt=torch.uint8)
+        nq = L.mep_moe_layer_queue_ints(N, E, H)
+        queue = self.queues.setdefault(nq, torch.zeros(nq, dtype=torch.int32, device="cuda"))
+        rc = L.mep_moe_layer(x.data_ptr(), w_r.data_ptr(), None, N, H, E, k, 1, w_in.data_ptr(), w_out.data_ptr(), I,
+                             idx.data_ptr(), gate.data_ptr(), None, counts.data_ptr(), offsets.data_ptr(),
+                             perm.data_ptr(), row.data_ptr(), None, y.data_ptr(), self.dws.data_ptr(),
+                             self.dws.numel(), act.data_ptr(), act.numel(), queue.data_ptr(), queue.numel(),
+                             out.data_ptr(), s)
+        if rc != 0:
+            raise RuntimeError(L.mep_last_error().decode())
+        torch.cuda.synchronize()
+        assert int(queue.abs().sum()) == 0
+        return out, idx, gate
+
+
+def test_raw_ctypes_moe_block_matches_ops():
+    """mep_moe_layer through raw ctypes at 32 tokens (one launch), then 7
+    (one launch), then 100 (router + dispatch, then the experts launch; the
+    dispatch workspace grows): each the bits of ops.moe_layer."""
+    raw = _RawBlock()
+    bf = torch.bfloat16
+    for n in (32, 7, 100):
+        banner(f"raw C ABI block (mep_moe_layer), {n} tokens")
+        layer = workloads.make_layer(n, seed=11 + n)
+        x, w_r, w_in, w_out = (t.to(bf).cuda() for t in (layer.x, layer.w_router, layer.w_in, layer.w_out))
+        out, idx, gate = raw(x, w_r, w_in, w_out)
+        ref, idx2, gate2, _ = ops.moe_layer(x, w_r, 8, w_in, w_out)
+        ops.experts_check()
+        assert torch.equal(idx, idx2) and torch.equal(gate, gate2)
+        assert torch.equal(out, ref)
 
 
 def test_error_codes_and_messages():
